@@ -1,0 +1,264 @@
+"""Benchmark: Block Sparse Attention forward at the 720p refinement shape.
+
+Default workload (one MI355X): B=1, 32 heads, S=57600 (16 x 45 x 80 latent
+grid, contiguous 64-token blocks -> 900 blocks), D=128, fp16, top-k = 57 KV
+blocks per q-block (ceil(0.0625 * 900); the reference's floor rule gives 56).
+Inputs are synthetic (seeded N(0,1) + per-block low-rank offsets, 3D RoPE,
+margin-repaired routing) and resident in HBM before timing starts.
+
+One step = one full BSA forward through the C ABI (pool q/k -> fused scores +
+top-k -> sparse attention), timed with HIP events on the launch stream.  A
+second timed pass launches the three stages separately to attribute time per
+kernel; the attention kernel's average duration gives the roofline line.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import re
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (str(REPO), str(REPO / "longcat-video-mlx_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "BSA fwd ms + executed-block TFLOP/s (% fp16 MFMA peak), S=57600 32h D128"
+PEAK_TFLOPS = {"f16": 2500.0, "bf16": 2500.0}  # MI355X dense MFMA peak
+DTYPE_NAME = {"float16": "f16", "bfloat16": "bf16", "float32": "f32"}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _traffic_from_profiles(workload: str):
+    """HBM bytes per attention launch from the committed rocprofv3 PMC summary."""
+    p = REPO / "profiles" / f"attn_fwd_{workload}_traffic.txt"
+    if not p.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(w, budget_s: float):
+    """The oracle (fp32 NumPy restatement of Tier A) on a bounded sample of the
+    same workload: pooling + routing for the sampled heads, then the gathered
+    attention for their q-blocks, until ``budget_s`` of CPU time is spent."""
+    import numpy as np
+
+    from oracle import bsa_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max(int(i.get("num_threads", 1)) for i in threadpool_info() if i.get("user_api") == "blas")
+    except Exception:  # pragma: no cover - threadpoolctl is optional
+        threads = os.cpu_count() or 1
+    B, H, S, D = w.q.shape
+    nb = S // 64
+    k = w.top_k
+    done_blocks, heads, t_total = 0, 0, 0.0
+    for b in range(B):
+        for h in range(H):
+            qh = w.q[b:b + 1, h:h + 1].float().cpu().numpy()
+            kh = w.k[b:b + 1, h:h + 1].float().cpu().numpy()
+            vh = w.v[b:b + 1, h:h + 1].float().cpu().numpy()
+            t0 = time.perf_counter()
+            qbar = O.mean_pool_blocks_3d(qh, w.shape, w.chunk_thw, acc=np.float32)
+            kbar = O.mean_pool_blocks_3d(kh, w.shape, w.chunk_thw, acc=np.float32)
+            idx, _ = O.topk_block_indices(O.block_routing_scores(qbar, kbar, acc=np.float32), top_k=k)
+            t_total += time.perf_counter() - t0
+            heads += 1
+            step = 64
+            for n0 in range(0, nb, step):
+                t0 = time.perf_counter()
+                O.sparse_attention_from_indices(qh, kh, vh, idx, w.shape, w.chunk_thw, w.sm_scale,
+                                                acc=np.float32, q_blocks=np.arange(n0, min(nb, n0 + step)))
+                t_total += time.perf_counter() - t0
+                done_blocks += min(nb, n0 + step) - n0
+                if t_total >= budget_s:
+                    break
+            if t_total >= budget_s:
+                break
+        if t_total >= budget_s:
+            break
+    flops = O.executed_flops(1, 1, done_blocks, k, D)
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": flops / t_total / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle fp32 (NumPy/OpenBLAS, {threads} threads, {cpu}): pool+route of {heads} "
+                   f"head(s) and sparse attention of {done_blocks} q-blocks x {k} KV blocks in "
+                   f"{t_total:.1f} s; full-workload estimate {t_total * (B * H * nb) / max(done_blocks, 1):.0f} s"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3"])
+    ap.add_argument("--top-k", type=int, default=None)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                          "(BSA shards by head across GPUs; see the design notes)"}))
+        log(f"bench.py: --gpus {args.gpus} requested, but only the single-GPU path exists")
+        return 2
+
+    import torch
+
+    from lcv_bsa import _lib
+    from lcv_bsa.block_sparse_attention import _geom, _strides
+    from lcv_bsa.workloads import CONFIGS, make_workload
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    cfg = CONFIGS[args.config]
+    top_k = args.top_k or cfg["top_k"]
+    t0 = time.time()
+    w = make_workload(args.config, dev, seed=args.seed, top_k=top_k,
+                      margin_ks=tuple(sorted({top_k, top_k - 1})))
+    torch.cuda.synchronize()
+    B, H, S, D = w.q.shape
+    nb = w.num_blocks
+    dtype = DTYPE_NAME[str(w.q.dtype).split(".")[1]]
+    log(f"workload {args.config}: B={B} H={H} S={S} D={D} {dtype} top_k={top_k} nb={nb} "
+        f"(margin repairs {w.repairs}, {time.time() - t0:.1f}s)")
+
+    code = {"f16": _lib.F16, "bf16": _lib.BF16, "f32": _lib.F32}[dtype]
+    out = torch.empty_like(w.q)
+    idx = torch.empty((B, H, nb, top_k), dtype=torch.int32, device=dev)
+    ws_bytes = lib.lcv_bsa_forward_workspace_bytes(B, H, nb, D)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    assert ws.data_ptr() % 256 == 0
+    qbar = ws[: ws_bytes // 2].view(torch.float32)
+    kbar = ws[ws_bytes // 2:].view(torch.float32)
+    geom = _geom(w.shape, w.chunk_thw)
+    qs, ks, vs, os_ = _strides(w.q), _strides(w.k), _strides(w.v), _strides(out)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def forward():
+        st = lib.lcv_bsa_forward(w.q.data_ptr(), w.k.data_ptr(), w.v.data_ptr(), code, B, H, S, D,
+                                 qs, ks, vs, top_k, w.sm_scale, geom, ws.data_ptr(), ws_bytes,
+                                 idx.data_ptr(), out.data_ptr(), os_, sh)
+        _lib.check(st, "lcv_bsa_forward")
+
+    def stage_pool():
+        _lib.check(lib.lcv_bsa_pool(w.q.data_ptr(), code, B, H, S, D, qs, geom, qbar.data_ptr(), sh), "pool q")
+        _lib.check(lib.lcv_bsa_pool(w.k.data_ptr(), code, B, H, S, D, ks, geom, kbar.data_ptr(), sh), "pool k")
+
+    def stage_select():
+        _lib.check(lib.lcv_bsa_select(qbar.data_ptr(), kbar.data_ptr(), B, H, nb, nb, D, top_k,
+                                      idx.data_ptr(), sh), "select")
+
+    def stage_attn():
+        _lib.check(lib.lcv_bsa_attn_fwd(w.q.data_ptr(), w.k.data_ptr(), w.v.data_ptr(), code, B, H, S,
+                                        D, qs, ks, vs, idx.data_ptr(), top_k, w.sm_scale, geom,
+                                        out.data_ptr(), os_, sh), "attn")
+
+    for _ in range(args.warmup):
+        forward()
+    torch.cuda.synchronize()
+
+    # Timed region 1: K full forwards.
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        forward()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+
+    # Timed region 2: the same work stage by stage, events between stages.
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for e in evs:
+        e[0].record(stream)
+        stage_pool()
+        e[1].record(stream)
+        stage_select()
+        e[2].record(stream)
+        stage_attn()
+        e[3].record(stream)
+    torch.cuda.synchronize()
+    ms_pool = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    ms_sel = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+    ms_attn = sum(e[2].elapsed_time(e[3]) for e in evs) / args.steps
+
+    flops = w.flops
+    tflops = flops / (ms_step * 1e-3) / 1e12
+    attn_tflops = flops / (ms_attn * 1e-3) / 1e12
+    peak = PEAK_TFLOPS.get(dtype, 2500.0)
+    workload = f"{args.config}_k{top_k}"
+    log(f"forward {ms_step:.3f} ms ({tflops:.1f} TFLOP/s executed-block); pool {ms_pool:.3f} ms, "
+        f"select {ms_sel:.3f} ms, attention {ms_attn:.3f} ms ({attn_tflops:.1f} TFLOP/s, "
+        f"{100 * attn_tflops / peak:.1f}% of {peak:.0f})")
+
+    result = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic (seeded N(0,1) + per-block low-rank offsets, 3D RoPE 44/42/42, margin-repaired routing)",
+        "config": {
+            "workload": f"bsa_fwd_{args.config}_B{B}_H{H}_S{S}_D{D}_{dtype}_topk{top_k}",
+            "B": B, "H": H, "S": S, "D": D, "num_blocks": nb, "block_tokens": 64,
+            "top_k": top_k, "top_k_rule": "ceil(0.0625*nb)" if top_k != max(1, int(0.0625 * nb)) else "floor (reference)",
+            "geometry": "shape=(1,1,S), chunk_thw=(1,1,64)",
+            "rope_grid": list(w.grid) if w.grid else None,
+            "executed_tflop": round(flops / 1e12, 4),
+        },
+        "breakdown_ms": {"pool": round(ms_pool, 4), "select": round(ms_sel, 4), "attention": round(ms_attn, 4)},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(attn_tflops, 2),
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": round(attn_tflops / peak, 4),
+            "traffic": _traffic_from_profiles(workload),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        t0 = time.time()
+        result["cpu_baseline"] = cpu_baseline(w, args.cpu_budget)
+        log(f"cpu baseline: {result['cpu_baseline']['value'] * 1e3:.2f} GFLOP/s ({time.time() - t0:.1f}s)")
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,193 @@
+/*
+ * lcv_bsa.h -- C ABI of the MI355X (gfx950) Block Sparse Attention forward.
+ *
+ * Every pointer argument is a DEVICE pointer unless stated otherwise.
+ * Dimensions are int64_t; strides are in ELEMENTS (not bytes) and the head
+ * dimension (last axis) must have stride 1.  `stream` is a hipStream_t passed
+ * as void* (NULL = the null stream).  Nothing here allocates or frees memory,
+ * synchronises the device, or retains a pointer past the call: outputs and
+ * workspaces are owned by the caller.  All launches are stream ordered.
+ *
+ * Tensor conventions follow the reference (longcat_video/models/
+ * block_sparse_attention.py): q, k, v are [B, H, S, D] with S = T*Hl*Wl
+ * flattened t-major over the latent grid (T, Hl, Wl).  A block is a
+ * cT x cH x cW voxel of that grid; blocks are numbered bt*Bh*Bw + bh*Bw + bw
+ * (Bt = T/cT, Bh = Hl/cH, Bw = Wl/cW) and the rows inside a block are ordered
+ * (i, j, l) row-major over the voxel (the reference's block-major order).
+ * Contiguous 64-token blocks are the grid (1, 1, S) with chunk (1, 1, 64).
+ *
+ * Return value: LCV_BSA_OK (0) or one of the LCV_BSA_ERR_* codes; the
+ * calling thread's last error text is available from lcv_bsa_last_error().
+ */
+#ifndef LCV_BSA_H
+#define LCV_BSA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of q / k / v / out. */
+enum lcv_bsa_dtype {
+  LCV_BSA_F16 = 0,
+  LCV_BSA_BF16 = 1,
+  LCV_BSA_F32 = 2
+};
+
+/* Status codes. */
+enum lcv_bsa_status {
+  LCV_BSA_OK = 0,
+  LCV_BSA_ERR_INVALID_ARG = 1,  /* null pointer, non-positive dimension   */
+  LCV_BSA_ERR_SHAPE = 2,        /* S != T*Hl*Wl, grid not a chunk multiple */
+  LCV_BSA_ERR_DTYPE = 3,        /* unknown dtype enum                       */
+  LCV_BSA_ERR_UNSUPPORTED = 4,  /* valid but unsupported (D, block size)    */
+  LCV_BSA_ERR_LAYOUT = 5,       /* stride / alignment the kernels can't use */
+  LCV_BSA_ERR_LAUNCH = 6        /* HIP runtime error at launch              */
+};
+
+/* Geometry of the latent grid and of one block (voxel). */
+typedef struct lcv_bsa_geom {
+  int64_t T, Hl, Wl;  /* latent grid; S must equal T*Hl*Wl   */
+  int64_t cT, cH, cW; /* voxel; each must divide its grid axis */
+} lcv_bsa_geom;
+
+/* Strides (in elements) of a [B, H, S, D] tensor whose D axis is dense. */
+typedef struct lcv_bsa_strides {
+  int64_t b, h, s;
+} lcv_bsa_strides;
+
+/* Library version string, e.g. "lcv_bsa 0.1.0 gfx950". Host only. */
+const char* lcv_bsa_version(void);
+
+/* Static text for a status code. Host only. */
+const char* lcv_bsa_strerror(int status);
+
+/* Detailed text of the calling thread's most recent failure ("" if none). */
+const char* lcv_bsa_last_error(void);
+
+/*
+ * Block-mean pooling.  out[b,h,n,:] = mean of the cT*cH*cW rows of block n,
+ * accumulated in fp32.  out is a dense [B, H, nb, D] fp32 tensor,
+ * nb = (T/cT)*(Hl/cH)*(Wl/cW).
+ * Replaces mean_pool_blocks_3d, longcat_video/models/block_sparse_attention.py:67-104
+ * (called from longcat_video/models/attention.py:103-104).
+ */
+int lcv_bsa_pool(const void* x, int dtype, int64_t B, int64_t H, int64_t S,
+                 int64_t D, lcv_bsa_strides xs, lcv_bsa_geom g, float* out,
+                 void* stream);
+
+/*
+ * Block routing scores: score[b,h,i,j] = dot(qbar[b,h,i,:], kbar[b,h,j,:])
+ * in fp32, unscaled.  qbar [B,H,nq,D], kbar [B,H,nk,D], score [B,H,nq,nk],
+ * all dense fp32.  D % 4 == 0, D <= 256.
+ * Replaces block_routing_scores, block_sparse_attention.py:107-112.
+ */
+int lcv_bsa_scores(const float* qbar, const float* kbar, int64_t B, int64_t H,
+                   int64_t nq, int64_t nk, int64_t D, float* score,
+                   void* stream);
+
+/*
+ * Per-row top-k of a dense fp32 score tensor [B,H,nq,nk] -> idx [B,H,nq,top_k]
+ * int32.  Each row's set is the top_k largest scores; among equal scores
+ * the lower block index wins; NaN ranks below -inf; -0.0 equals +0.0.
+ * Indices are written in ascending order.  1 <= top_k <= nk <= 4096.
+ * Replaces topk_block_indices, block_sparse_attention.py:115-134
+ * (the reference returns the same set in unspecified order).
+ */
+int lcv_bsa_topk(const float* score, int64_t B, int64_t H, int64_t nq,
+                 int64_t nk, int64_t top_k, int32_t* idx, void* stream);
+
+/*
+ * Fused routing: scores of qbar x kbar^T kept on chip, then the per-row
+ * top-k of lcv_bsa_topk.  Same arguments and result as lcv_bsa_scores
+ * followed by lcv_bsa_topk, without the [B,H,nq,nk] intermediate.
+ * Replaces block_sparse_attention.py:230-233 (attention.py:105-108).
+ */
+int lcv_bsa_select(const float* qbar, const float* kbar, int64_t B, int64_t H,
+                   int64_t nq, int64_t nk, int64_t D, int64_t top_k,
+                   int32_t* idx, void* stream);
+
+/*
+ * Sparse attention over given block lists (the kernel-level entry):
+ *   out[b,h,s,:] = softmax_j(sm_scale * q[s].k[j]) v[j]
+ * over every key j in the blocks idx[b,h,block_of(s),0..top_k-1].
+ * Entries < 0 or >= nb are skipped (padding); a row with no valid block
+ * gets zeros.  Duplicate entries are attended once per occurrence (the
+ * reference kernels' behaviour).  idx is a dense [B,H,nb,top_k] int32.
+ * Blocks must hold 64 tokens.  D in {16,32,64,128,256} (MFMA path for
+ * fp16/bf16 with D in {64,128}; other combinations use a vector-ALU path).
+ * Replaces bsa_attention_metal_v4 / _v3 / _v2 / bsa_attention_metal,
+ * longcat_video/models/block_sparse_attention_metal.py:985-1046 (and
+ * 729-810, 484-548, 224-295): their block-major reshapes (185-221) are
+ * folded into the kernel's row addressing.
+ */
+int lcv_bsa_attn_fwd(const void* q, const void* k, const void* v, int dtype,
+                     int64_t B, int64_t H, int64_t S, int64_t D,
+                     lcv_bsa_strides qs, lcv_bsa_strides ks,
+                     lcv_bsa_strides vs, const int32_t* idx, int64_t top_k,
+                     float sm_scale, lcv_bsa_geom g, void* out,
+                     lcv_bsa_strides os, void* stream);
+
+/*
+ * Bytes of fp32 workspace lcv_bsa_forward needs: the pooled means of q and
+ * k, 2*B*H*nb*D*4 bytes.  Host only.
+ */
+size_t lcv_bsa_forward_workspace_bytes(int64_t B, int64_t H, int64_t nb,
+                                       int64_t D);
+
+/*
+ * End-to-end block sparse attention: pool q and k, route (scores + top-k),
+ * then sparse attention.  idx receives the [B,H,nb,top_k] routing
+ * (ascending per row); workspace holds at least
+ * lcv_bsa_forward_workspace_bytes() bytes, 256-byte aligned.
+ * Replaces bsa_attention, block_sparse_attention.py:201-250, whose result
+ * equals this one (its masked entries contribute exactly zero).
+ */
+int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype,
+                    int64_t B, int64_t H, int64_t S, int64_t D,
+                    lcv_bsa_strides qs, lcv_bsa_strides ks,
+                    lcv_bsa_strides vs, int64_t top_k, float sm_scale,
+                    lcv_bsa_geom g, void* workspace, size_t workspace_bytes,
+                    int32_t* idx, void* out, lcv_bsa_strides os,
+                    void* stream);
+
+/*
+ * Token -> block map: out[s] = block of token s (int32, length T*Hl*Wl).
+ * Replaces build_token_block_indices, block_sparse_attention.py:137-159.
+ */
+int lcv_bsa_token_blocks(lcv_bsa_geom g, int32_t* out, void* stream);
+
+/*
+ * Token-pair mask: mask[b,h,sq,sk] = 1 if token_block[sk] is listed in
+ * idx[b,h,token_block[sq],:], else 0 (uint8, dense [B,H,S,S]).
+ * idx is a dense [B,H,nq,top_k] int32 routing, token_block a length-S int32
+ * map into [0, nq) (as lcv_bsa_token_blocks writes); num_kv_blocks bounds the
+ * listed entries (those outside [0, num_kv_blocks) match nothing).  Only
+ * sensible for small S (B*H*S*S <= 2^34).
+ * Replaces build_token_pair_mask, block_sparse_attention.py:162-198.
+ */
+int lcv_bsa_token_pair_mask(const int32_t* idx, int64_t B, int64_t H,
+                            int64_t nq, int64_t top_k,
+                            const int32_t* token_block, int64_t S,
+                            int64_t num_kv_blocks, uint8_t* mask,
+                            void* stream);
+
+/*
+ * t-major <-> block-major row permutation of a [B,H,S,D] tensor (dense in
+ * and out, same dtype).  inverse = 0: out row (block n, row r) = x row of
+ * that token; inverse = 1: the reverse.
+ * Replaces _reshape_to_block_major / _reshape_from_block_major,
+ * block_sparse_attention_metal.py:185-221.
+ */
+int lcv_bsa_permute_block_major(const void* x, int dtype, int64_t B,
+                                int64_t H, int64_t S, int64_t D,
+                                lcv_bsa_geom g, int inverse, void* out,
+                                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LCV_BSA_H */

@@ -1,0 +1,331 @@
+// C ABI entry points: argument validation, geometry checks and launches.
+//
+// The shape contract mirrors the reference's ValueError checks
+// (longcat_video/models/block_sparse_attention.py:86-96 and
+// longcat_video/models/block_sparse_attention_metal.py:257-262, 1003-1017):
+// a violation returns LCV_BSA_ERR_SHAPE / _UNSUPPORTED with the reason in
+// lcv_bsa_last_error(), which the Python layer turns into ValueError.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <cmath>
+
+#include "bsa_common.h"
+
+#define LCV_BSA_VERSION "lcv_bsa 0.1.0 gfx950"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int ok() {
+  g_last_error[0] = '\0';
+  return LCV_BSA_OK;
+}
+
+int launch_status(hipError_t e, const char* what) {
+  if (e != hipSuccess)
+    return fail(LCV_BSA_ERR_LAUNCH, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+  return ok();
+}
+
+bool dtype_ok(int dtype) {
+  return dtype == LCV_BSA_F16 || dtype == LCV_BSA_BF16 || dtype == LCV_BSA_F32;
+}
+
+int elem_bytes(int dtype) { return dtype == LCV_BSA_F32 ? 4 : 2; }
+
+constexpr int64_t kI32Max = 2147483647;
+
+// Validates (B, H, S, D) and the grid/voxel geometry; fills nb and bs.
+int check_geom(int64_t B, int64_t H, int64_t S, int64_t D, const lcv_bsa_geom& g, int64_t* nb,
+               int64_t* bs) {
+  if (B <= 0 || H <= 0 || S <= 0 || D <= 0)
+    return fail(LCV_BSA_ERR_INVALID_ARG, "B, H, S, D must be positive (got %lld, %lld, %lld, %lld)",
+                (long long)B, (long long)H, (long long)S, (long long)D);
+  if (g.T <= 0 || g.Hl <= 0 || g.Wl <= 0 || g.cT <= 0 || g.cH <= 0 || g.cW <= 0)
+    return fail(LCV_BSA_ERR_INVALID_ARG, "grid and chunk extents must be positive");
+  if (g.T % g.cT || g.Hl % g.cH || g.Wl % g.cW)
+    return fail(LCV_BSA_ERR_SHAPE,
+                "Latent shape (%lld, %lld, %lld) must be a multiple of chunk_thw (%lld, %lld, %lld)",
+                (long long)g.T, (long long)g.Hl, (long long)g.Wl, (long long)g.cT, (long long)g.cH,
+                (long long)g.cW);
+  if (S != g.T * g.Hl * g.Wl)
+    return fail(LCV_BSA_ERR_SHAPE, "S=%lld doesn't match T*H*W=%lld", (long long)S,
+                (long long)(g.T * g.Hl * g.Wl));
+  if (S > kI32Max / 2 || B * H > kI32Max / 4)
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "S=%lld or B*H=%lld too large", (long long)S,
+                (long long)(B * H));
+  *bs = g.cT * g.cH * g.cW;
+  *nb = S / *bs;
+  if (B * H * (*nb) > kI32Max)
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "B*H*num_blocks too large");
+  return LCV_BSA_OK;
+}
+
+int check_strides(const char* name, const lcv_bsa_strides& s, int64_t D) {
+  if (s.b < 0 || s.h < 0 || s.s < D)
+    return fail(LCV_BSA_ERR_LAYOUT,
+                "%s strides (b=%lld, h=%lld, s=%lld) must be non-negative with s >= D=%lld "
+                "(the head dimension must be dense)",
+                name, (long long)s.b, (long long)s.h, (long long)s.s, (long long)D);
+  return LCV_BSA_OK;
+}
+
+bool vec_aligned(const void* p, const lcv_bsa_strides& s, int vec) {
+  return ((uintptr_t)p & 15u) == 0 && s.b % vec == 0 && s.h % vec == 0 && s.s % vec == 0;
+}
+
+int check_attn_args(const void* q, const void* k, const void* v, const void* out, int dtype,
+                    int64_t B, int64_t H, int64_t S, int64_t D, const lcv_bsa_strides& qs,
+                    const lcv_bsa_strides& ks, const lcv_bsa_strides& vs,
+                    const lcv_bsa_strides& os, int64_t top_k, float sm_scale,
+                    const lcv_bsa_geom& g, int64_t* nb, int64_t* bs) {
+  if (!q || !k || !v || !out) return fail(LCV_BSA_ERR_INVALID_ARG, "null tensor pointer");
+  if (!dtype_ok(dtype)) return fail(LCV_BSA_ERR_DTYPE, "unknown dtype %d", dtype);
+  int st = check_geom(B, H, S, D, g, nb, bs);
+  if (st) return st;
+  if (*bs != 64)
+    return fail(LCV_BSA_ERR_UNSUPPORTED,
+                "block size cT*cH*cW=%lld: the attention kernels require 64-token blocks",
+                (long long)*bs);
+  if (!lcv::attn_supported(dtype, (int)D))
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "head_dim D=%lld unsupported (D in {16,32,64,128,256})",
+                (long long)D);
+  if (top_k < 1 || top_k > kI32Max / (*nb))
+    return fail(LCV_BSA_ERR_INVALID_ARG, "top_k=%lld must be >= 1", (long long)top_k);
+  if (!std::isfinite(sm_scale)) return fail(LCV_BSA_ERR_INVALID_ARG, "sm_scale must be finite");
+  if ((st = check_strides("q", qs, D)) || (st = check_strides("k", ks, D)) ||
+      (st = check_strides("v", vs, D)) || (st = check_strides("out", os, D)))
+    return st;
+  if (lcv::attn_uses_mfma(dtype, (int)D)) {
+    const int vec = 16 / elem_bytes(dtype);
+    if (!vec_aligned(q, qs, vec) || !vec_aligned(k, ks, vec) || !vec_aligned(v, vs, vec) ||
+        ((uintptr_t)out & 7u) || os.b % 4 || os.h % 4 || os.s % 4)
+      return fail(LCV_BSA_ERR_LAYOUT,
+                  "q/k/v rows must start on 16-byte boundaries and out rows on 8-byte "
+                  "boundaries (strides multiples of 8 / 4 elements)");
+  }
+  return LCV_BSA_OK;
+}
+
+lcv::AttnParams make_attn_params(const void* q, const void* k, const void* v, void* out,
+                                 const lcv_bsa_strides& qs, const lcv_bsa_strides& ks,
+                                 const lcv_bsa_strides& vs, const lcv_bsa_strides& os,
+                                 const int32_t* idx, int64_t B, int64_t H, int64_t nb,
+                                 int64_t top_k, float sm_scale, const lcv_bsa_geom& g) {
+  lcv::AttnParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.out = out;
+  p.q_sb = qs.b, p.q_sh = qs.h, p.q_ss = qs.s;
+  p.k_sb = ks.b, p.k_sh = ks.h, p.k_ss = ks.s;
+  p.v_sb = vs.b, p.v_sh = vs.h, p.v_ss = vs.s;
+  p.o_sb = os.b, p.o_sh = os.h, p.o_ss = os.s;
+  p.idx = idx;
+  p.B = (int32_t)B;
+  p.H = (int32_t)H;
+  p.nb = (int32_t)nb;
+  p.top_k = (int32_t)top_k;
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  p.g = lcv::make_geom(g);
+  return p;
+}
+
+int check_route(int64_t B, int64_t H, int64_t nq, int64_t nk, int64_t D, bool need_d) {
+  if (B <= 0 || H <= 0 || nq <= 0 || nk <= 0 || (need_d && D <= 0))
+    return fail(LCV_BSA_ERR_INVALID_ARG, "B, H, nq, nk%s must be positive", need_d ? ", D" : "");
+  if (B * H * nq > kI32Max || nq * nk > kI32Max)
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "routing problem too large");
+  if (!lcv::select_supported((int)nk, need_d ? (int)D : 4))
+    return fail(LCV_BSA_ERR_UNSUPPORTED,
+                "routing supports nk <= 4096 and D % 4 == 0, D <= 128 (got nk=%lld, D=%lld)",
+                (long long)nk, (long long)D);
+  return LCV_BSA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* lcv_bsa_version(void) { return LCV_BSA_VERSION; }
+
+const char* lcv_bsa_strerror(int status) {
+  switch (status) {
+    case LCV_BSA_OK: return "ok";
+    case LCV_BSA_ERR_INVALID_ARG: return "invalid argument";
+    case LCV_BSA_ERR_SHAPE: return "shape mismatch";
+    case LCV_BSA_ERR_DTYPE: return "unsupported dtype";
+    case LCV_BSA_ERR_UNSUPPORTED: return "unsupported configuration";
+    case LCV_BSA_ERR_LAYOUT: return "unsupported memory layout";
+    case LCV_BSA_ERR_LAUNCH: return "kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+const char* lcv_bsa_last_error(void) { return g_last_error; }
+
+int lcv_bsa_pool(const void* x, int dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                 lcv_bsa_strides xs, lcv_bsa_geom g, float* out, void* stream) {
+  if (!x || !out) return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
+  if (!dtype_ok(dtype)) return fail(LCV_BSA_ERR_DTYPE, "unknown dtype %d", dtype);
+  int64_t nb = 0, bs = 0;
+  int st = check_geom(B, H, S, D, g, &nb, &bs);
+  if (st) return st;
+  if ((st = check_strides("x", xs, D))) return st;
+  const lcv::Tensor4 t{x, xs.b, xs.h, xs.s};
+  float* outs[1] = {out};
+  return launch_status(lcv::launch_pool(&t, 1, dtype, (int)B, (int)H, (int)D, (int)nb, (int)bs,
+                                        lcv::make_geom(g), outs, (hipStream_t)stream),
+                       "lcv_bsa_pool");
+}
+
+int lcv_bsa_scores(const float* qbar, const float* kbar, int64_t B, int64_t H, int64_t nq,
+                   int64_t nk, int64_t D, float* score, void* stream) {
+  if (!qbar || !kbar || !score) return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
+  int st = check_route(B, H, nq, nk, D, true);
+  if (st) return st;
+  return launch_status(lcv::launch_scores(qbar, kbar, (int)B, (int)H, (int)nq, (int)nk, (int)D,
+                                          score, (hipStream_t)stream),
+                       "lcv_bsa_scores");
+}
+
+int lcv_bsa_topk(const float* score, int64_t B, int64_t H, int64_t nq, int64_t nk, int64_t top_k,
+                 int32_t* idx, void* stream) {
+  if (!score || !idx) return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
+  int st = check_route(B, H, nq, nk, 0, false);
+  if (st) return st;
+  if (top_k < 1 || top_k > nk)
+    return fail(LCV_BSA_ERR_INVALID_ARG, "top_k=%lld must be in [1, nk=%lld]", (long long)top_k,
+                (long long)nk);
+  return launch_status(lcv::launch_topk(score, (int)B, (int)H, (int)nq, (int)nk, (int)top_k, idx,
+                                        (hipStream_t)stream),
+                       "lcv_bsa_topk");
+}
+
+int lcv_bsa_select(const float* qbar, const float* kbar, int64_t B, int64_t H, int64_t nq,
+                   int64_t nk, int64_t D, int64_t top_k, int32_t* idx, void* stream) {
+  if (!qbar || !kbar || !idx) return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
+  int st = check_route(B, H, nq, nk, D, true);
+  if (st) return st;
+  if (top_k < 1 || top_k > nk)
+    return fail(LCV_BSA_ERR_INVALID_ARG, "top_k=%lld must be in [1, nk=%lld]", (long long)top_k,
+                (long long)nk);
+  return launch_status(lcv::launch_select(qbar, kbar, (int)B, (int)H, (int)nq, (int)nk, (int)D,
+                                          (int)top_k, idx, (hipStream_t)stream),
+                       "lcv_bsa_select");
+}
+
+int lcv_bsa_attn_fwd(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                     int64_t H, int64_t S, int64_t D, lcv_bsa_strides qs, lcv_bsa_strides ks,
+                     lcv_bsa_strides vs, const int32_t* idx, int64_t top_k, float sm_scale,
+                     lcv_bsa_geom g, void* out, lcv_bsa_strides os, void* stream) {
+  int64_t nb = 0, bs = 0;
+  int st = check_attn_args(q, k, v, out, dtype, B, H, S, D, qs, ks, vs, os, top_k, sm_scale, g,
+                           &nb, &bs);
+  if (st) return st;
+  if (!idx) return fail(LCV_BSA_ERR_INVALID_ARG, "null block index pointer");
+  const lcv::AttnParams p =
+      make_attn_params(q, k, v, out, qs, ks, vs, os, idx, B, H, nb, top_k, sm_scale, g);
+  return launch_status(lcv::launch_attn(p, dtype, (int)D, (hipStream_t)stream),
+                       "lcv_bsa_attn_fwd");
+}
+
+size_t lcv_bsa_forward_workspace_bytes(int64_t B, int64_t H, int64_t nb, int64_t D) {
+  if (B <= 0 || H <= 0 || nb <= 0 || D <= 0) return 0;
+  const size_t one = (size_t)B * H * nb * D * sizeof(float);
+  const size_t one_aligned = (one + 255) & ~(size_t)255;
+  return 2 * one_aligned;
+}
+
+int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                    int64_t S, int64_t D, lcv_bsa_strides qs, lcv_bsa_strides ks,
+                    lcv_bsa_strides vs, int64_t top_k, float sm_scale, lcv_bsa_geom g,
+                    void* workspace, size_t workspace_bytes, int32_t* idx, void* out,
+                    lcv_bsa_strides os, void* stream) {
+  int64_t nb = 0, bs = 0;
+  int st = check_attn_args(q, k, v, out, dtype, B, H, S, D, qs, ks, vs, os, top_k, sm_scale, g,
+                           &nb, &bs);
+  if (st) return st;
+  if (!idx || !workspace) return fail(LCV_BSA_ERR_INVALID_ARG, "null idx or workspace pointer");
+  if (top_k > nb)
+    return fail(LCV_BSA_ERR_INVALID_ARG, "top_k=%lld exceeds num_blocks=%lld", (long long)top_k,
+                (long long)nb);
+  if ((st = check_route(B, H, nb, nb, D, true))) return st;
+  const size_t need = lcv_bsa_forward_workspace_bytes(B, H, nb, D);
+  if (workspace_bytes < need || ((uintptr_t)workspace & 255u))
+    return fail(LCV_BSA_ERR_INVALID_ARG,
+                "workspace must be 256-byte aligned and hold %zu bytes (got %zu)", need,
+                workspace_bytes);
+  hipStream_t s = (hipStream_t)stream;
+  float* qbar = reinterpret_cast<float*>(workspace);
+  float* kbar = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + need / 2);
+  const lcv::Tensor4 ts[2] = {{q, qs.b, qs.h, qs.s}, {k, ks.b, ks.h, ks.s}};
+  float* outs[2] = {qbar, kbar};
+  const lcv::Geom gg = lcv::make_geom(g);
+  st = launch_status(lcv::launch_pool(ts, 2, dtype, (int)B, (int)H, (int)D, (int)nb, (int)bs, gg,
+                                      outs, s),
+                     "lcv_bsa_forward(pool)");
+  if (st) return st;
+  st = launch_status(lcv::launch_select(qbar, kbar, (int)B, (int)H, (int)nb, (int)nb, (int)D,
+                                        (int)top_k, idx, s),
+                     "lcv_bsa_forward(select)");
+  if (st) return st;
+  const lcv::AttnParams p =
+      make_attn_params(q, k, v, out, qs, ks, vs, os, idx, B, H, nb, top_k, sm_scale, g);
+  return launch_status(lcv::launch_attn(p, dtype, (int)D, s), "lcv_bsa_forward(attn)");
+}
+
+int lcv_bsa_token_blocks(lcv_bsa_geom g, int32_t* out, void* stream) {
+  if (!out) return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
+  int64_t nb = 0, bs = 0;
+  const int64_t S = g.T * g.Hl * g.Wl;
+  int st = check_geom(1, 1, S > 0 ? S : 1, 1, g, &nb, &bs);
+  if (st) return st;
+  return launch_status(lcv::launch_token_blocks(lcv::make_geom(g), (int)g.T, out,
+                                                (hipStream_t)stream),
+                       "lcv_bsa_token_blocks");
+}
+
+int lcv_bsa_token_pair_mask(const int32_t* idx, int64_t B, int64_t H, int64_t nq,
+                            int64_t top_k, const int32_t* token_block, int64_t S,
+                            int64_t num_kv_blocks, uint8_t* mask, void* stream) {
+  if (!idx || !token_block || !mask) return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
+  if (B <= 0 || H <= 0 || nq <= 0 || top_k <= 0 || S <= 0 || num_kv_blocks <= 0)
+    return fail(LCV_BSA_ERR_INVALID_ARG, "B, H, nq, top_k, S, num_kv_blocks must be positive");
+  if (S > kI32Max || nq > kI32Max || num_kv_blocks > kI32Max || B * H * nq * top_k > kI32Max * 8 ||
+      B * H * S * S > ((int64_t)1 << 34))
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "token-pair mask of %lld entries is too large",
+                (long long)(B * H * S * S));
+  return launch_status(lcv::launch_pair_mask(idx, (int)B, (int)H, (int)nq, (int)top_k,
+                                             token_block, (int)S, (int)num_kv_blocks, mask,
+                                             (hipStream_t)stream),
+                       "lcv_bsa_token_pair_mask");
+}
+
+int lcv_bsa_permute_block_major(const void* x, int dtype, int64_t B, int64_t H, int64_t S,
+                                int64_t D, lcv_bsa_geom g, int inverse, void* out,
+                                void* stream) {
+  if (!x || !out) return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
+  if (!dtype_ok(dtype)) return fail(LCV_BSA_ERR_DTYPE, "unknown dtype %d", dtype);
+  int64_t nb = 0, bs = 0;
+  int st = check_geom(B, H, S, D, g, &nb, &bs);
+  if (st) return st;
+  if (B * H * S * D > ((int64_t)1 << 38))
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "tensor too large");
+  return launch_status(lcv::launch_permute(x, elem_bytes(dtype), (int)B, (int)H, (int)S, (int)D,
+                                           lcv::make_geom(g), inverse ? 1 : 0, out,
+                                           (hipStream_t)stream),
+                       "lcv_bsa_permute_block_major");
+}
+
+}  // extern "C"

@@ -1,0 +1,247 @@
+// Block routing: fp32 block scores qbar . kbar^T and per-row top-k.
+//
+// Follows block_routing_scores + topk_block_indices
+// (longcat_video/models/block_sparse_attention.py:107-134).  The reference
+// materialises the [B,H,nq,nk] score tensor and runs argpartition; here a
+// wave computes whole score rows straight into registers in the layout its
+// top-k needs (lane l holds columns l, l+64, l+128, ...), so the fused path
+// never writes scores to memory.
+//
+// Top-k is an exact radix select on order-preserving 32-bit keys: a 32-step
+// binary search finds the k-th largest key with ballot/popcount counts, then
+// one ordered pass emits the indices of keys above it plus the lowest-index
+// keys equal to it, in ascending index order.  Equal scores therefore resolve
+// to the lower block index; NaN ranks below -inf; -0.0 equals +0.0.
+#include "bsa_common.h"
+
+namespace lcv {
+namespace {
+
+constexpr int kMaxD = 128;       // pooled head dim supported by the routing kernels
+constexpr int kKeyChunk = 64;    // keys staged per LDS chunk (one per lane)
+constexpr int kMaxPer = 64;      // max score columns per lane -> nk <= 4096
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+  if (f != f) return 0u;       // NaN: below every number
+  if (f == 0.0f) f = 0.0f;     // -0.0 -> +0.0
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Exact top-k of one score row held as sc[e] = score[e*64 + lane], e < NPER.
+// Writes the k selected column indices, ascending, to out[0..k).
+template <int NPER>
+__device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out) {
+  const int lane = lane_id();
+  uint32_t key[NPER];
+#pragma unroll
+  for (int e = 0; e < NPER; ++e) {
+    const int col = e * 64 + lane;
+    key[e] = col < nk ? order_key(sc[e]) : 0u;
+  }
+  // Largest threshold t with #(key >= t) >= k, built bit by bit.  Padding
+  // columns carry key 0 and never reach a candidate >= 1.
+  uint32_t thr = 0u;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = thr | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int e = 0; e < NPER; ++e) cnt += __popcll(ballot64(key[e] >= cand));
+    if (cnt >= k) thr = cand;
+  }
+  int gt = 0;
+#pragma unroll
+  for (int e = 0; e < NPER; ++e) gt += __popcll(ballot64(key[e] > thr));
+  const int need_eq = k - gt;  // >= 1
+  int run_sel = 0, run_eq = 0;
+#pragma unroll
+  for (int e = 0; e < NPER; ++e) {
+    const int col = e * 64 + lane;
+    const bool valid = col < nk;
+    const bool is_gt = valid && key[e] > thr;
+    const bool is_eq = valid && key[e] == thr;
+    const uint64_t eqm = ballot64(is_eq);
+    const int eq_rank = run_eq + (int)mbcnt64(eqm);
+    const bool sel = is_gt || (is_eq && eq_rank < need_eq);
+    const uint64_t selm = ballot64(sel);
+    if (sel) out[run_sel + (int)mbcnt64(selm)] = col;
+    run_sel += __popcll(selm);
+    run_eq += __popcll(eqm);
+  }
+}
+
+struct RouteArgs {
+  const float* qbar;
+  const float* kbar;
+  const float* score_in;
+  float* score_out;
+  int32_t* idx;
+  int32_t H, nq, nk, D, top_k;
+  int32_t tiles_per_bh;
+};
+
+enum RouteMode { kSelect = 0, kScoresOnly = 1, kTopkOnly = 2 };
+
+// One workgroup = 4 waves x RW score rows of one (b, h).  Lane l of a wave
+// owns score columns e*64 + l; the 64 kbar rows of chunk e are staged in LDS
+// (row stride D+4 floats: conflict-free 16-byte reads), the workgroup's qbar
+// rows are read as LDS broadcasts.
+template <int NPER, int RW, int MODE>
+__global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
+  __shared__ __attribute__((aligned(16))) float kch[kKeyChunk * (kMaxD + 4)];
+  __shared__ __attribute__((aligned(16))) float qt[4 * RW * kMaxD];
+  const int tid = threadIdx.x;
+  const int wave = tid / 64;
+  const int lane = tid % 64;
+  const int bh = blockIdx.x / a.tiles_per_bh;
+  const int tile = blockIdx.x - bh * a.tiles_per_bh;
+  const int row0 = tile * (4 * RW) + wave * RW;  // this wave's first row
+  const int D = a.D;
+  const int KS = D + 4;
+  float sc[RW][NPER];
+
+  if (MODE == kTopkOnly) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int row = row0 + r;
+      const float* src = a.score_in + ((int64_t)bh * a.nq + (row < a.nq ? row : 0)) * a.nk;
+#pragma unroll
+      for (int e = 0; e < NPER; ++e) {
+        const int col = e * 64 + lane;
+        sc[r][e] = (row < a.nq && col < a.nk) ? src[col] : 0.0f;
+      }
+    }
+  } else {
+    const float* qb = a.qbar + (int64_t)bh * a.nq * D;
+    const float* kb = a.kbar + (int64_t)bh * a.nk * D;
+    const int D4 = D / 4;
+    const int wg_row0 = tile * (4 * RW);
+    for (int i = tid; i < 4 * RW * D4; i += 256) {
+      const int r = i / D4;
+      const int c = i - r * D4;
+      const int row = wg_row0 + r;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (row < a.nq) v = *reinterpret_cast<const f32x4*>(qb + (int64_t)row * D + 4 * c);
+      *reinterpret_cast<f32x4*>(qt + r * D + 4 * c) = v;
+    }
+#pragma unroll
+    for (int e = 0; e < NPER; ++e) {
+      __syncthreads();  // previous chunk fully consumed; qt visible
+      for (int i = tid; i < kKeyChunk * D4; i += 256) {
+        const int kr = i / D4;
+        const int c = i - kr * D4;
+        const int key = e * kKeyChunk + kr;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (key < a.nk) v = *reinterpret_cast<const f32x4*>(kb + (int64_t)key * D + 4 * c);
+        *reinterpret_cast<f32x4*>(kch + kr * KS + 4 * c) = v;
+      }
+      __syncthreads();
+      float acc[RW];
+#pragma unroll
+      for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+      const float* krow = kch + lane * KS;
+      for (int d = 0; d < D; d += 4) {
+        const f32x4 kv = *reinterpret_cast<const f32x4*>(krow + d);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          const f32x4 qv = *reinterpret_cast<const f32x4*>(qt + (wave * RW + r) * D + d);
+          acc[r] = fmaf(qv[0], kv[0], acc[r]);
+          acc[r] = fmaf(qv[1], kv[1], acc[r]);
+          acc[r] = fmaf(qv[2], kv[2], acc[r]);
+          acc[r] = fmaf(qv[3], kv[3], acc[r]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RW; ++r) sc[r][e] = acc[r];
+    }
+  }
+
+  if (MODE == kScoresOnly) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int row = row0 + r;
+      if (row >= a.nq) continue;
+      float* dst = a.score_out + ((int64_t)bh * a.nq + row) * a.nk;
+#pragma unroll
+      for (int e = 0; e < NPER; ++e) {
+        const int col = e * 64 + lane;
+        if (col < a.nk) dst[col] = sc[r][e];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int row = row0 + r;
+      if (row >= a.nq) continue;  // wave-uniform
+      wave_topk<NPER>(sc[r], a.nk, a.top_k, a.idx + ((int64_t)bh * a.nq + row) * a.top_k);
+    }
+  }
+}
+
+template <int NPER, int MODE>
+hipError_t launch_route_n(RouteArgs a, int BH, hipStream_t stream) {
+  constexpr int RW = NPER <= 16 ? 4 : (NPER == 32 ? 2 : 1);
+  a.tiles_per_bh = (a.nq + 4 * RW - 1) / (4 * RW);
+  hipLaunchKernelGGL((route_kernel<NPER, RW, MODE>), dim3(BH * a.tiles_per_bh), dim3(256), 0,
+                     stream, a);
+  return hipGetLastError();
+}
+
+template <int MODE>
+hipError_t launch_route(RouteArgs a, int BH, hipStream_t stream) {
+  const int per = (a.nk + 63) / 64;
+  if (per <= 1) return launch_route_n<1, MODE>(a, BH, stream);
+  if (per <= 2) return launch_route_n<2, MODE>(a, BH, stream);
+  if (per <= 4) return launch_route_n<4, MODE>(a, BH, stream);
+  if (per <= 8) return launch_route_n<8, MODE>(a, BH, stream);
+  if (per <= 16) return launch_route_n<16, MODE>(a, BH, stream);
+  if (per <= 32) return launch_route_n<32, MODE>(a, BH, stream);
+  return launch_route_n<64, MODE>(a, BH, stream);
+}
+
+}  // namespace
+
+bool select_supported(int nk, int D) {
+  return nk >= 1 && nk <= kMaxPer * 64 && D >= 4 && D <= kMaxD && D % 4 == 0;
+}
+
+hipError_t launch_scores(const float* qbar, const float* kbar, int B, int H, int nq, int nk,
+                         int D, float* score, hipStream_t stream) {
+  RouteArgs a{};
+  a.qbar = qbar;
+  a.kbar = kbar;
+  a.score_out = score;
+  a.H = H;
+  a.nq = nq;
+  a.nk = nk;
+  a.D = D;
+  return launch_route<kScoresOnly>(a, B * H, stream);
+}
+
+hipError_t launch_topk(const float* score, int B, int H, int nq, int nk, int top_k,
+                       int32_t* idx, hipStream_t stream) {
+  RouteArgs a{};
+  a.score_in = score;
+  a.idx = idx;
+  a.H = H;
+  a.nq = nq;
+  a.nk = nk;
+  a.top_k = top_k;
+  return launch_route<kTopkOnly>(a, B * H, stream);
+}
+
+hipError_t launch_select(const float* qbar, const float* kbar, int B, int H, int nq, int nk,
+                         int D, int top_k, int32_t* idx, hipStream_t stream) {
+  RouteArgs a{};
+  a.qbar = qbar;
+  a.kbar = kbar;
+  a.idx = idx;
+  a.H = H;
+  a.nq = nq;
+  a.nk = nk;
+  a.D = D;
+  a.top_k = top_k;
+  return launch_route<kSelect>(a, B * H, stream);
+}
+
+}  // namespace lcv

@@ -1,0 +1,49 @@
+"""Shared test setup: import paths, the ``gpu`` marker, small helpers."""
+
+from __future__ import annotations
+
+import os
+import sys
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+PKG_ROOT = REPO / "longcat-video-mlx_amd"
+for p in (str(REPO), str(PKG_ROOT)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line(
+        "markers", "gpu: needs an MI355X (gfx950) device; runs the HIP kernels")
+
+
+@pytest.fixture(scope="session")
+def device():
+    """cuda:0 with the native library loaded.  GPU tests fail (not skip) on a
+    machine without a device, so they can never pass silently."""
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test selected but no ROCm device is visible")
+    from lcv_bsa import _lib
+
+    _lib.load()  # raises if liblcv_bsa.so is missing
+    return torch.device("cuda", 0)
+
+
+def assert_close_report(actual, expected, max_abs: float, mean_abs: float, what: str = ""):
+    """max-abs / mean-abs parity check with a readable report."""
+    import numpy as np
+
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    assert a.shape == e.shape, f"{what}: shape {a.shape} != {e.shape}"
+    assert np.isfinite(a).all(), f"{what}: non-finite values in result"
+    d = np.abs(a - e)
+    mx, mn = float(d.max()), float(d.mean())
+    assert mx <= max_abs and mn <= mean_abs, (
+        f"{what}: max_abs={mx:.3e} (tol {max_abs:.1e}) mean_abs={mn:.3e} (tol {mean_abs:.1e})")
+    return mx, mn

@@ -1,0 +1,330 @@
+"""CPU tests of the host side: the C-ABI library loads and exports what
+include/lcv_bsa.h declares, its argument validation (paths that return before
+any launch), the dispatcher / enable_bsa wiring (mirroring
+tests/smoke/test_bsa_dit_wiring_smoke.py) and the workload generator."""
+
+from __future__ import annotations
+
+import math
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bsa_oracle as O
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "lcv_bsa.h"
+NO_GPU = not torch.cuda.is_available()
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int|size_t)\s+(lcv_bsa_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    from lcv_bsa import _lib
+
+    assert _declared() == sorted(_lib.EXPORTED)
+
+
+def test_library_loads_and_exports_every_symbol():
+    import ctypes
+
+    from lcv_bsa import _lib
+
+    lib = _lib.load()
+    for name in _declared():
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+    assert "gfx950" in _lib.version()
+    for code in range(7):
+        assert lib.lcv_bsa_strerror(code)
+    assert lib.lcv_bsa_strerror(99) == b"unknown status"
+
+
+@pytest.mark.skipif(not NO_GPU, reason="validation-only calls use fake pointers; CPU container only")
+def test_c_abi_validation_returns_before_launch():
+    """Each call below must be rejected by argument checks (no launch)."""
+    from lcv_bsa import _lib
+
+    lib = _lib.load()
+    S_ = _lib.Strides
+    G = _lib.Geom
+    fake = 4096  # never dereferenced: every call fails validation first
+    st = lib.lcv_bsa_pool(None, 0, 1, 1, 64, 8, S_(512, 512, 8), G(4, 4, 4, 4, 4, 4), fake, None)
+    assert st == _lib.ERR_INVALID_ARG
+    st = lib.lcv_bsa_pool(fake, 0, 1, 1, 96, 8, S_(768, 768, 8), G(4, 4, 6, 4, 4, 4), fake, None)
+    assert st == _lib.ERR_SHAPE and b"multiple of" in lib.lcv_bsa_last_error()
+    st = lib.lcv_bsa_pool(fake, 0, 1, 1, 100, 8, S_(800, 800, 8), G(4, 4, 4, 4, 4, 4), fake, None)
+    assert st == _lib.ERR_SHAPE and b"doesn't match" in lib.lcv_bsa_last_error()
+    st = lib.lcv_bsa_pool(fake, 7, 1, 1, 64, 8, S_(512, 512, 8), G(4, 4, 4, 4, 4, 4), fake, None)
+    assert st == _lib.ERR_DTYPE
+    args = dict(B=1, H=1, S=64, D=128)
+    st = lib.lcv_bsa_attn_fwd(fake, fake, fake, 0, 1, 1, 64, 128, S_(8192, 8192, 128),
+                              S_(8192, 8192, 128), S_(8192, 8192, 128), fake, 0, 0.1,
+                              G(4, 4, 4, 4, 4, 4), fake, S_(8192, 8192, 128), None)
+    assert st == _lib.ERR_INVALID_ARG  # top_k = 0
+    st = lib.lcv_bsa_attn_fwd(fake, fake, fake, 0, 1, 1, 8, 128, S_(1024, 1024, 128),
+                              S_(1024, 1024, 128), S_(1024, 1024, 128), fake, 1, 0.1,
+                              G(2, 2, 2, 2, 2, 2), fake, S_(1024, 1024, 128), None)
+    assert st == _lib.ERR_UNSUPPORTED and b"64-token" in lib.lcv_bsa_last_error()
+    st = lib.lcv_bsa_attn_fwd(fake, fake, fake, 0, 1, 1, 64, 24, S_(1536, 1536, 24),
+                              S_(1536, 1536, 24), S_(1536, 1536, 24), fake, 1, 0.1,
+                              G(4, 4, 4, 4, 4, 4), fake, S_(1536, 1536, 24), None)
+    assert st == _lib.ERR_UNSUPPORTED and b"head_dim" in lib.lcv_bsa_last_error()
+    st = lib.lcv_bsa_attn_fwd(fake + 2, fake, fake, 0, 1, 1, 64, 128, S_(8192, 8192, 128),
+                              S_(8192, 8192, 128), S_(8192, 8192, 128), fake, 1, 0.1,
+                              G(4, 4, 4, 4, 4, 4), fake, S_(8192, 8192, 128), None)
+    assert st == _lib.ERR_LAYOUT
+    st = lib.lcv_bsa_attn_fwd(fake, fake, fake, 0, 1, 1, 64, 128, S_(8192, 8192, 64),
+                              S_(8192, 8192, 128), S_(8192, 8192, 128), fake, 1, 0.1,
+                              G(4, 4, 4, 4, 4, 4), fake, S_(8192, 8192, 128), None)
+    assert st == _lib.ERR_LAYOUT  # row stride below D
+    st = lib.lcv_bsa_topk(fake, 1, 1, 4, 8, 9, fake, None)
+    assert st == _lib.ERR_INVALID_ARG  # top_k > nk
+    st = lib.lcv_bsa_select(fake, fake, 1, 1, 4, 5000, 64, 4, fake, None)
+    assert st == _lib.ERR_UNSUPPORTED  # nk > 4096
+    st = lib.lcv_bsa_select(fake, fake, 1, 1, 4, 8, 6, 4, fake, None)
+    assert st == _lib.ERR_UNSUPPORTED  # D % 4
+    ws = lib.lcv_bsa_forward_workspace_bytes(1, 32, 900, 128)
+    assert ws == 2 * 32 * 900 * 128 * 4
+    st = lib.lcv_bsa_forward(fake, fake, fake, 0, 1, 1, 4096, 128, S_(1 << 19, 1 << 19, 128),
+                             S_(1 << 19, 1 << 19, 128), S_(1 << 19, 1 << 19, 128), 4, 0.1,
+                             G(1, 1, 4096, 1, 1, 64), fake, 16, fake, fake,
+                             S_(1 << 19, 1 << 19, 128), None)
+    assert st == _lib.ERR_INVALID_ARG and b"workspace" in lib.lcv_bsa_last_error()
+    with pytest.raises(ValueError, match="multiple of"):
+        _lib.check(lib.lcv_bsa_pool(fake, 0, 1, 1, 96, 8, S_(768, 768, 8), G(4, 4, 6, 4, 4, 4),
+                                    fake, None), "pool")
+
+
+def test_python_api_rejects_cpu_tensors_loudly():
+    """No silent CPU path: host tensors raise (not a ValueError, so the
+    dispatcher cannot turn it into a dense fallback)."""
+    from lcv_bsa import bsa_attention
+    from lcv_bsa.block_sparse_attention import BSADeviceError
+
+    q = torch.zeros((1, 1, 64, 16))
+    with pytest.raises(BSADeviceError):
+        bsa_attention(q, q, q, shape=(4, 4, 4))
+    assert not issubclass(BSADeviceError, ValueError)
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from lcv_bsa import _lib
+
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "missing.so")
+    with pytest.raises(ImportError, match="no fallback"):
+        _lib.load()
+
+
+# ---------------------------------------------------------------------------
+# Dispatcher and model wiring (test_bsa_dit_wiring_smoke.py)
+# ---------------------------------------------------------------------------
+
+class _Block:
+    def __init__(self):
+        from lcv_bsa import BSAAttention
+
+        self.attn = BSAAttention(64, 4)
+
+
+class _Model:
+    def __init__(self, config):
+        from lcv_bsa import BSAModelMixin, apply_bsa_params
+
+        self.blocks = [_Block() for _ in range(config["depth"])]
+        apply_bsa_params(self, config)
+
+    def enable_bsa(self, backend="hip"):
+        from lcv_bsa import enable_bsa
+
+        enable_bsa(self, backend)
+
+    def disable_bsa(self):
+        from lcv_bsa import disable_bsa
+
+        disable_bsa(self)
+
+
+def _config(enable=False):
+    return {"depth": 2, "bsa_params": {"sparsity": 0.9375, "chunk_3d_shape_q": [4, 4, 4],
+                                       "chunk_3d_shape_k": [4, 4, 4]}, "enable_bsa": enable}
+
+
+def test_default_bsa_off():
+    assert all(b.attn.enable_bsa is False for b in _Model(_config(False)).blocks)
+
+
+def test_config_enable_bsa_flips_attention():
+    m = _Model(_config(True))
+    for b in m.blocks:
+        assert b.attn.enable_bsa is True
+        assert b.attn.bsa_sparsity == 0.9375 and b.attn.bsa_chunk_thw == (4, 4, 4)
+        assert b.attn.bsa_backend == "hip"
+
+
+def test_enable_disable_roundtrip():
+    m = _Model(_config(False))
+    m.enable_bsa()
+    assert all(b.attn.enable_bsa for b in m.blocks)
+    m.disable_bsa()
+    assert not any(b.attn.enable_bsa for b in m.blocks)
+
+
+def test_bsa_params_preserved_through_enable():
+    cfg = _config(False)
+    cfg["bsa_params"]["sparsity"] = 0.5
+    cfg["bsa_params"]["chunk_3d_shape_q"] = [2, 2, 2]
+    m = _Model(cfg)
+    m.enable_bsa()
+    assert all(b.attn.bsa_sparsity == 0.5 and b.attn.bsa_chunk_thw == (2, 2, 2) for b in m.blocks)
+
+
+def test_backend_validation():
+    from lcv_bsa.attention import validate_backend
+
+    assert validate_backend("hip") == "hip"
+    with pytest.raises(AssertionError, match="MLX/Metal"):
+        validate_backend("metal_v4")
+    with pytest.raises(AssertionError, match="unknown BSA backend"):
+        validate_backend("cuda")
+    m = _Model(_config(False))
+    with pytest.raises(AssertionError):
+        m.enable_bsa("tier_a")
+
+
+def test_env_var_default_and_override(monkeypatch):
+    from lcv_bsa.attention import backend_from_env
+
+    monkeypatch.delenv("LONGCAT_BSA_BACKEND", raising=False)
+    assert backend_from_env() == "hip"
+    monkeypatch.setenv("LONGCAT_BSA_BACKEND", "hip")
+    assert backend_from_env() == "hip"
+
+
+def test_process_attn_dense_path_on_cpu():
+    """BSA off, or shape None: dense SDPA with scale head_dim**-0.5 (attention.py:179)."""
+    from lcv_bsa import BSAAttention
+
+    a = BSAAttention(4 * 16, 4)
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(1, 4, 64, 16, generator=g) for _ in range(3))
+    out = a._process_attn(q, k, v, shape=(4, 4, 4))
+    assert a.last_path == "dense"
+    ref = O.sdpa(q.numpy(), k.numpy(), v.numpy(), 0.25)
+    assert np.abs(out.numpy() - ref).max() < 1e-5
+    a.enable_bsa = True
+    out = a._process_attn(q, k, v, shape=None)
+    assert a.last_path == "dense"
+
+
+# ---------------------------------------------------------------------------
+# Count rules and the workload generator
+# ---------------------------------------------------------------------------
+
+def test_count_rules():
+    from lcv_bsa import num_selected_blocks
+    from lcv_bsa.workloads import top_k_ceil, top_k_floor
+
+    assert num_selected_blocks(900, 0.9375) == 56 == top_k_floor(900, 0.9375)
+    assert top_k_ceil(900, 0.9375) == 57 and top_k_ceil(450, 0.9375) == 29
+    assert [top_k_ceil(900, s) for s in (0.875, 0.9375, 0.96875)] == [113, 57, 29]
+    assert [top_k_floor(900, s) for s in (0.875, 0.9375, 0.96875)] == [112, 56, 28]
+    assert top_k_ceil(8, 0.75) == 2 and top_k_floor(4, 0.99) == 1
+
+
+def test_executed_flops_headline():
+    from lcv_bsa.workloads import executed_flops
+
+    f = executed_flops(1, 32, 900, 57, 128)
+    assert f == 4 * 32 * 900 * 57 * 64 * 64 * 128
+    assert abs(f / 1e12 - 3.4427) < 1e-3
+    assert abs(executed_flops(1, 32, 450, 29, 128) / 1e12 - 0.8758) < 1e-3
+
+
+def test_block_tokens_matches_oracle():
+    from lcv_bsa.workloads import block_tokens
+
+    for shape, chunk in [((8, 12, 16), (4, 4, 4)), ((1, 1, 512), (1, 1, 64)), ((4, 6, 8), (2, 3, 4))]:
+        assert np.array_equal(block_tokens(shape, chunk).numpy(), O.block_tokens(shape, chunk))
+
+
+def test_rope_matches_oracle():
+    from lcv_bsa.rope_3d import rope_3d, rope_freqs_3d, rope_dims
+
+    assert rope_dims(128) == (44, 42, 42)
+    grid = (3, 5, 7)
+    f = rope_freqs_3d(grid, 128).numpy()
+    fo = O.rope_freqs_3d(grid, 128)
+    assert np.allclose(f, fo, rtol=1e-6, atol=1e-6)
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(1, 2, 105, 128, generator=g)
+    qr, _ = rope_3d(q, q, grid)
+    assert np.allclose(qr.numpy(), O.apply_rope(q.numpy(), fo), atol=2e-5)
+
+
+def test_inputs_margins_and_determinism():
+    from lcv_bsa.workloads import make_inputs
+
+    shape, chunk, ks = (1, 1, 4096), (1, 1, 64), (3, 4)
+    q, k, v, info = make_inputs(1, 2, 64, shape, chunk, torch.float16, "cpu", seed=5,
+                                grid=(4, 16, 64), margin_ks=ks)
+    q2, k2, v2, _ = make_inputs(1, 2, 64, shape, chunk, torch.float16, "cpu", seed=5,
+                                grid=(4, 16, 64), margin_ks=ks)
+    assert torch.equal(q, q2) and torch.equal(k, k2) and torch.equal(v, v2)
+    assert q.dtype == torch.float16
+    sc = O.block_routing_scores(O.mean_pool_blocks_3d(q.float().numpy(), shape, chunk),
+                                O.mean_pool_blocks_3d(k.float().numpy(), shape, chunk))
+    top = -np.sort(-sc, axis=-1)
+    for kk in ks:
+        assert (top[..., kk - 1] - top[..., kk]).min() > 1e-4
+    print("repairs", info["repairs"], "rounds", info["rounds"])
+
+
+def test_inputs_voxel_geometry_offsets():
+    """The low-rank offset is added per voxel block (block_tokens mapping)."""
+    from lcv_bsa.workloads import make_inputs
+
+    shape, chunk = (8, 8, 8), (4, 4, 4)
+    q, k, v, info = make_inputs(1, 1, 32, shape, chunk, torch.float32, "cpu", seed=1,
+                                offset_std=50.0)
+    qb = O.mean_pool_blocks_3d(q.numpy(), shape, chunk)
+    # the offset dominates each voxel's mean; rows of one voxel share it
+    bt = O.block_tokens(shape, chunk)
+    U = info["U"].numpy()
+    for n in range(bt.shape[0]):
+        proj = q.numpy()[0, 0, bt[n]] @ U.T  # [64, 4]
+        assert np.abs(proj.mean(0) - qb[0, 0, n] @ U.T).max() < 1e-3
+        assert proj.std(0).max() < 3.0  # N(0,1) noise around a shared offset
+
+
+# ---------------------------------------------------------------------------
+# Golden fixtures: the oracle and the generator still reproduce them
+# ---------------------------------------------------------------------------
+
+def test_golden_c0_reproduced():
+    from lcv_bsa.workloads import make_workload
+
+    fx = np.load(REPO / "tests" / "golden" / "c0.npz")
+    w = make_workload("c0", "cpu", seed=int(fx["seed"]))
+    assert float(w.q.double().sum()) == pytest.approx(float(fx["q_sum"]), abs=1e-6)
+    q, k, v = (t.numpy() for t in (w.q, w.k, w.v))
+    out, idx = O.bsa_attention(q, k, v, w.shape, 0.9375, w.chunk_thw, top_k=int(fx["top_k"]),
+                               return_indices=True)
+    assert np.array_equal(idx, fx["indices"])
+    assert np.abs(out[:, :, fx["rows"]] - fx["out_rows"]).max() < 1e-12
+
+
+def test_golden_voxel_reproduced():
+    fx = np.load(REPO / "tests" / "golden" / "voxel.npz")
+    shape, chunk = tuple(fx["shape"]), tuple(fx["chunk"])
+    q, k, v = (fx[n].astype(np.float32) for n in ("q", "k", "v"))
+    out, idx = O.bsa_attention_masked(q, k, v, shape, float(fx["sparsity"]), chunk,
+                                      return_indices=True)
+    assert np.array_equal(idx, fx["indices"])
+    assert np.abs(out - fx["out"]).max() < 1e-6

@@ -1,0 +1,321 @@
+"""GPU parity of each native kernel against the oracle, through the C ABI.
+
+Mirrors the reference's kernel gates (tests/smoke/test_bsa_tier_b_smoke.py)
+and adds exact checks for the integer/index work.  Tolerances (attention
+output vs the fp64 oracle on the same, already-rounded inputs):
+  fp16 : max-abs 2e-3, mean-abs 2e-4
+  bf16 : max-abs 1e-2, mean-abs 2e-3 (P and the output carry 8-bit mantissas)
+  fp32 : max-abs 2e-5, mean-abs 2e-6
+Block indices, token maps, masks and permutations must be bit-exact.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_report
+from oracle import bsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = {
+    torch.float16: (2e-3, 2e-4),
+    torch.bfloat16: (1e-2, 2e-3),
+    torch.float32: (2e-5, 2e-6),
+}
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy() if t.dtype != torch.float64 else t.cpu().numpy()
+
+
+def _rand(shape, dtype, device, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dtype).to(device)
+
+
+def _distinct_indices(B, H, nq, nk, k, seed, sort=True):
+    rng = np.random.default_rng(seed)
+    out = np.empty((B, H, nq, k), dtype=np.int32)
+    for b in range(B):
+        for h in range(H):
+            for i in range(nq):
+                sel = rng.choice(nk, size=k, replace=False)
+                out[b, h, i] = np.sort(sel) if sort else sel
+    return out
+
+
+def test_library_version(device):
+    from lcv_bsa import _lib
+
+    v = _lib.version()
+    print("library:", v)
+    assert "gfx950" in v
+
+
+# ---------------------------------------------------------------------------
+# Pooling (block_sparse_attention.py:67-104)
+# ---------------------------------------------------------------------------
+
+POOL_CASES = [
+    ((1, 1, 4096), (1, 1, 64), 64),
+    ((8, 12, 16), (4, 4, 4), 128),
+    ((4, 8, 8), (2, 2, 2), 32),
+    ((8, 8, 8), (4, 4, 4), 4),
+    ((2, 6, 10), (1, 2, 5), 24),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape,chunk,D", POOL_CASES)
+def test_pool_matches_oracle(device, dtype, shape, chunk, D):
+    from lcv_bsa import mean_pool_blocks_3d
+
+    S = int(np.prod(shape))
+    x = _rand((2, 3, S, D), dtype, device, seed=S + D)
+    got = mean_pool_blocks_3d(x, shape, chunk)
+    ref = O.mean_pool_blocks_3d(_np(x), shape, chunk)
+    assert got.dtype == torch.float32
+    assert_close_report(_np(got), ref, 2e-6, 2e-7, f"pool {shape} {chunk} D={D} {dtype}")
+
+
+def test_pool_strided_view(device):
+    """q as the DiT produces it: a [B,H,S,D] view of a [B,S,H,D] buffer."""
+    from lcv_bsa import mean_pool_blocks_3d
+
+    base = _rand((1, 4096, 4, 128), torch.float16, device, seed=5)
+    x = base.transpose(1, 2)
+    assert not x.is_contiguous() and x.stride(3) == 1
+    got = mean_pool_blocks_3d(x, (1, 1, 4096), (1, 1, 64))
+    ref = O.mean_pool_blocks_3d(_np(x.contiguous()), (1, 1, 4096), (1, 1, 64))
+    assert_close_report(_np(got), ref, 2e-6, 2e-7, "pool strided")
+
+
+def test_pool_rejects_bad_shape(device):
+    from lcv_bsa import mean_pool_blocks_3d
+
+    x = torch.zeros((1, 1, 96, 8), device=device)
+    with pytest.raises(ValueError, match="multiple of"):
+        mean_pool_blocks_3d(x, (4, 4, 6), (4, 4, 4))
+    with pytest.raises(ValueError, match="doesn't match"):
+        mean_pool_blocks_3d(torch.zeros((1, 1, 100, 8), device=device), (4, 4, 4))
+
+
+# ---------------------------------------------------------------------------
+# Scores and top-k (block_sparse_attention.py:107-134)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("nq,nk,D", [(1, 1, 4), (7, 63, 16), (64, 64, 64), (65, 65, 128),
+                                     (100, 900, 128), (33, 2049, 32), (5, 4096, 8)])
+def test_scores_match_oracle(device, nq, nk, D):
+    from lcv_bsa import block_routing_scores
+
+    qb = _rand((2, 2, nq, D), torch.float32, device, seed=nq)
+    kb = _rand((2, 2, nk, D), torch.float32, device, seed=nk + 1)
+    got = _np(block_routing_scores(qb, kb))
+    ref = O.block_routing_scores(_np(qb), _np(kb))
+    assert_close_report(got, ref, 2e-5 * math.sqrt(D), 2e-6 * math.sqrt(D), f"scores {nq}x{nk}x{D}")
+
+
+def test_scores_known_answer(device):
+    """test_bsa_tier_a_smoke.py:68-75."""
+    from lcv_bsa import block_routing_scores
+
+    s = block_routing_scores(torch.ones((1, 1, 4, 8), device=device),
+                             2 * torch.ones((1, 1, 4, 8), device=device))
+    assert s.shape == (1, 1, 4, 4) and float(s[0, 0, 0, 0]) == 16.0
+
+
+@pytest.mark.parametrize("nk", [1, 5, 64, 65, 127, 450, 900, 2048, 4096])
+def test_topk_exact_with_ties(device, nk):
+    """Integer-valued scores: many exact ties, resolved toward the lower index."""
+    from lcv_bsa import topk_block_indices
+
+    rng = np.random.default_rng(nk)
+    sc = rng.integers(-20, 21, size=(2, 3, 17, nk)).astype(np.float32)
+    sc[0, 0, 0] = -0.0
+    sc[0, 0, 1] = np.nan
+    sc[0, 0, 2, ::2] = np.nan
+    sc[0, 0, 3] = -np.inf
+    sc[0, 0, 4, :nk // 2] = np.inf
+    sct = torch.from_numpy(sc).to(device)
+    for k in sorted({1, max(1, nk // 16), max(1, nk // 2), nk}):
+        got, kk = topk_block_indices(sct, 0.0, top_k=k)
+        ref, _ = O.topk_block_indices(sc, top_k=k)
+        assert kk == k
+        assert np.array_equal(got.cpu().numpy(), ref), f"nk={nk} k={k}"
+
+
+def test_topk_count_rule(device):
+    """test_bsa_tier_a_smoke.py:78-94 on the HIP top-k."""
+    from lcv_bsa import topk_block_indices
+
+    idx, n = topk_block_indices(_rand((1, 2, 4, 8), torch.float32, device, 1), sparsity=0.75)
+    assert n == 2 and idx.shape == (1, 2, 4, 2)
+    a = idx.cpu().numpy()
+    assert (a >= 0).all() and (a < 8).all()
+    _, n1 = topk_block_indices(_rand((1, 1, 2, 4), torch.float32, device, 2), sparsity=0.99)
+    assert n1 == 1
+
+
+@pytest.mark.parametrize("nq,nk,D,k", [(64, 64, 64, 4), (450, 450, 128, 29), (900, 900, 128, 57),
+                                       (17, 1000, 16, 999), (3, 3000, 128, 187)])
+def test_select_fused_equals_two_step(device, nq, nk, D, k):
+    """Fused routing == scores + top-k (same fp32 products), and == the oracle
+    on integer-valued means (exact in fp32, exact ties)."""
+    from lcv_bsa import block_routing_scores, select_block_indices, topk_block_indices
+
+    qb = _rand((1, 2, nq, D), torch.float32, device, seed=3 * nq)
+    kb = _rand((1, 2, nk, D), torch.float32, device, seed=5 * nk)
+    fused = select_block_indices(qb, kb, k)
+    two, _ = topk_block_indices(block_routing_scores(qb, kb), 0.0, top_k=k)
+    assert torch.equal(fused, two)
+    qi, ki = torch.round(qb * 2), torch.round(kb * 2)
+    fused_i = select_block_indices(qi, ki, k).cpu().numpy()
+    ref, _ = O.topk_block_indices(O.block_routing_scores(_np(qi), _np(ki)), top_k=k)
+    assert np.array_equal(fused_i, ref)
+
+
+# ---------------------------------------------------------------------------
+# Sparse attention from given indices (block_sparse_attention_metal.py contract)
+# ---------------------------------------------------------------------------
+
+ATTN_GEOMS = [
+    ((1, 1, 512), (1, 1, 64)),
+    ((8, 8, 16), (4, 4, 4)),
+    ((2, 12, 16), (1, 4, 16)),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("geom", ATTN_GEOMS)
+def test_attn_matches_oracle(device, dtype, D, geom):
+    from lcv_bsa import bsa_attention_hip
+
+    shape, chunk = geom
+    S = int(np.prod(shape))
+    nb = S // 64
+    B, H = 2, 2
+    q, k, v = (_rand((B, H, S, D), dtype, device, seed=s) for s in (11, 12, 13))
+    for topk in sorted({1, 3, nb}):
+        idx = _distinct_indices(B, H, nb, nb, topk, seed=topk, sort=(topk != 3))
+        out = bsa_attention_hip(q, k, v, torch.from_numpy(idx).to(device), chunk, shape)
+        ref = O.sparse_attention_from_indices(_np(q), _np(k), _np(v), idx, shape, chunk)
+        assert out.dtype == dtype
+        assert_close_report(_np(out), ref, *TOL[dtype], f"attn {dtype} D={D} {geom} k={topk}")
+
+
+@pytest.mark.parametrize("D", [16, 32, 256])
+def test_attn_valu_head_dims(device, D):
+    from lcv_bsa import bsa_attention_hip
+
+    shape, chunk = (1, 1, 256), (1, 1, 64)
+    q, k, v = (_rand((1, 2, 256, D), torch.float16, device, seed=s) for s in (1, 2, 3))
+    idx = _distinct_indices(1, 2, 4, 4, 2, seed=D)
+    out = bsa_attention_hip(q, k, v, torch.from_numpy(idx).to(device), chunk, shape)
+    ref = O.sparse_attention_from_indices(_np(q), _np(k), _np(v), idx, shape, chunk)
+    assert_close_report(_np(out), ref, *TOL[torch.float16], f"attn valu D={D}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_attn_single_block_equals_dense(device, dtype):
+    """test_bsa_tier_b_smoke.py:47-79 / :388-433: one block, top_k=1 == dense SDPA."""
+    from lcv_bsa import bsa_attention_hip
+
+    D = 128 if dtype == torch.float16 else 16
+    q, k, v = (_rand((1, 2, 64, D), dtype, device, seed=s) for s in (0, 1, 2))
+    out = bsa_attention_hip(q, k, v, torch.zeros((1, 2, 1, 1), dtype=torch.int32, device=device),
+                            (4, 4, 4), (4, 4, 4))
+    dense = torch.nn.functional.scaled_dot_product_attention(
+        q.float().cpu(), k.float().cpu(), v.float().cpu(), scale=1.0 / math.sqrt(D))
+    assert_close_report(_np(out), dense.numpy(), *TOL[dtype], f"single block {dtype}")
+
+
+def test_attn_padding_and_duplicates(device):
+    from lcv_bsa import bsa_attention_hip
+
+    shape, chunk = (1, 1, 256), (1, 1, 64)
+    q, k, v = (_rand((1, 1, 256, 128), torch.float16, device, seed=s) for s in (4, 5, 6))
+    idx = np.array([[[[0, -1, 2], [1, 1, 3], [-1, -1, -1], [7, 3, 0]]]], dtype=np.int32)
+    out = bsa_attention_hip(q, k, v, torch.from_numpy(idx).to(device), chunk, shape)
+    ref = O.sparse_attention_from_indices(_np(q), _np(k), _np(v), idx, shape, chunk)
+    assert_close_report(_np(out), ref, *TOL[torch.float16], "padding/duplicates")
+    assert (out[0, 0, 128:192] == 0).all()
+
+
+def test_attn_strided_views_and_determinism(device):
+    from lcv_bsa import bsa_attention_hip
+
+    S, H, D = 1024, 4, 128
+    buf = _rand((3, 1, S, H, D), torch.float16, device, seed=9)
+    q, k, v = (buf[i].transpose(1, 2) for i in range(3))  # [1,H,S,D] views, stride(3)==1
+    idx = torch.from_numpy(_distinct_indices(1, H, 16, 16, 5, seed=9)).to(device)
+    o1 = bsa_attention_hip(q, k, v, idx, (1, 1, 64), (1, 1, S))
+    o2 = bsa_attention_hip(q.contiguous(), k.contiguous(), v.contiguous(), idx, (1, 1, 64), (1, 1, S))
+    assert torch.equal(o1, o2)
+    o3 = bsa_attention_hip(q, k, v, idx, (1, 1, 64), (1, 1, S))
+    assert torch.equal(o1, o3)
+
+
+def test_attn_contract_errors(device):
+    """test_bsa_tier_b_smoke.py:163-175 and the shape=None rule."""
+    from lcv_bsa import bsa_attention_hip
+
+    z = torch.zeros((1, 1, 48, 16), device=device)
+    bi = torch.zeros((1, 1, 1, 1), dtype=torch.int32, device=device)
+    with pytest.raises(ValueError, match="multiple of"):
+        bsa_attention_hip(z, z, z, bi, (4, 4, 4), (4, 4, 4))
+    z64 = torch.zeros((1, 1, 64, 16), device=device)
+    with pytest.raises(ValueError, match="shape"):
+        bsa_attention_hip(z64, z64, z64, bi, (4, 4, 4), None)
+    z8 = torch.zeros((1, 1, 8, 16), device=device)
+    with pytest.raises(ValueError, match="block_size=64"):
+        bsa_attention_hip(z8, z8, z8, bi, (2, 2, 2), (2, 2, 2))
+    z24 = torch.zeros((1, 1, 64, 24), device=device)
+    with pytest.raises(ValueError, match="head_dim"):
+        bsa_attention_hip(z24, z24, z24, bi, (4, 4, 4), (4, 4, 4))
+
+
+# ---------------------------------------------------------------------------
+# Index / layout helpers (exact)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape,chunk", [((4, 4, 4), (4, 4, 4)), ((8, 4, 4), (4, 4, 4)),
+                                         ((6, 8, 12), (2, 4, 3)), ((1, 1, 57600), (1, 1, 64))])
+def test_token_blocks_exact(device, shape, chunk):
+    from lcv_bsa import build_token_block_indices
+
+    got = build_token_block_indices(shape, chunk, device=device).cpu().numpy()
+    assert np.array_equal(got, O.build_token_block_indices(shape, chunk))
+
+
+def test_token_pair_mask_exact(device):
+    from lcv_bsa import build_token_block_indices, build_token_pair_mask
+
+    # the reference's known answer, test_bsa_tier_a_smoke.py:114-138
+    bi = np.array([[[[3, 5], [0, 7]]]], dtype=np.int32)
+    tbi = np.arange(8, dtype=np.int32)
+    got = build_token_pair_mask(torch.from_numpy(bi).to(device), torch.from_numpy(tbi).to(device), 8)
+    assert np.array_equal(got.cpu().numpy(), O.build_token_pair_mask(bi, tbi, 8))
+    # a routed voxel geometry
+    shape, chunk = (8, 8, 8), (4, 4, 4)
+    idx = _distinct_indices(1, 2, 8, 8, 3, seed=1)
+    tb = build_token_block_indices(shape, chunk, device=device)
+    got = build_token_pair_mask(torch.from_numpy(idx).to(device), tb, 8).cpu().numpy()
+    assert np.array_equal(got, O.build_token_pair_mask(idx, O.build_token_block_indices(shape, chunk), 8))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_block_major_permutation_exact(device, dtype):
+    from lcv_bsa import reshape_from_block_major, reshape_to_block_major
+
+    shape, chunk = (8, 12, 16), (4, 4, 4)
+    x = _rand((1, 2, 8 * 12 * 16, 32), dtype, device, seed=2)
+    bm = reshape_to_block_major(x, shape, chunk)
+    assert np.array_equal(_np(bm), O.reshape_to_block_major(_np(x), shape, chunk))
+    assert torch.equal(reshape_from_block_major(bm, shape, chunk), x)
