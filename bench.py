@@ -120,7 +120,23 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a device-to-device copy of MIB MiB (a known-size kernel "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
+
+    if args.calibrate_copy:
+        import torch
+
+        n = args.calibrate_copy * (1 << 20)
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": n, "launches": 3}))
+        return 0
 
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -155,8 +171,10 @@ def main() -> int:
     ws_bytes = lib.lcv_bsa_forward_workspace_bytes(B, H, nb, D)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     assert ws.data_ptr() % 256 == 0
-    qbar = ws[: ws_bytes // 2].view(torch.float32)
-    kbar = ws[ws_bytes // 2:].view(torch.float32)
+    pooled = (B * H * nb * D * 4 + 255) // 256 * 256  # workspace layout: qbar, kbar, order
+    qbar = ws[:pooled].view(torch.float32)
+    kbar = ws[pooled:2 * pooled].view(torch.float32)
+    order = ws[2 * pooled:2 * pooled + B * H * nb * 4].view(torch.int32)
     geom = _geom(w.shape, w.chunk_thw)
     qs, ks, vs, os_ = _strides(w.q), _strides(w.k), _strides(w.v), _strides(out)
     stream = torch.cuda.current_stream(dev)
@@ -175,11 +193,13 @@ def main() -> int:
     def stage_select():
         _lib.check(lib.lcv_bsa_select(qbar.data_ptr(), kbar.data_ptr(), B, H, nb, nb, D, top_k,
                                       idx.data_ptr(), sh), "select")
+        _lib.check(lib.lcv_bsa_schedule(idx.data_ptr(), B, H, nb, top_k, order.data_ptr(), sh),
+                   "schedule")
 
     def stage_attn():
         _lib.check(lib.lcv_bsa_attn_fwd(w.q.data_ptr(), w.k.data_ptr(), w.v.data_ptr(), code, B, H, S,
-                                        D, qs, ks, vs, idx.data_ptr(), top_k, w.sm_scale, geom,
-                                        out.data_ptr(), os_, sh), "attn")
+                                        D, qs, ks, vs, idx.data_ptr(), order.data_ptr(), top_k,
+                                        w.sm_scale, geom, out.data_ptr(), os_, sh), "attn")
 
     for _ in range(args.warmup):
         forward()
@@ -241,7 +261,7 @@ def main() -> int:
             "rope_grid": list(w.grid) if w.grid else None,
             "executed_tflop": round(flops / 1e12, 4),
         },
-        "breakdown_ms": {"pool": round(ms_pool, 4), "select": round(ms_sel, 4), "attention": round(ms_attn, 4)},
+        "breakdown_ms": {"pool": round(ms_pool, 4), "select_and_schedule": round(ms_sel, 4), "attention": round(ms_attn, 4)},
         "roofline": {
             "bound": "mfma",
             "achieved": round(attn_tflops, 2),

@@ -110,12 +110,25 @@ int lcv_bsa_select(const float* qbar, const float* kbar, int64_t B, int64_t H,
                    int32_t* idx, void* stream);
 
 /*
+ * Launch order for lcv_bsa_attn_fwd: per (b,h), a permutation of the nq
+ * q-blocks sorted by (first, middle) entry of their routing lists, so that
+ * q-blocks whose ascending lists start together run together and share K/V
+ * tiles in L2.  order is a dense [B,H,nq] int32.  Any permutation gives the
+ * same attention result; this one only changes speed.  nq <= 4096.
+ * No counterpart in the reference (its kernels launch in block order).
+ */
+int lcv_bsa_schedule(const int32_t* idx, int64_t B, int64_t H, int64_t nq,
+                     int64_t top_k, int32_t* order, void* stream);
+
+/*
  * Sparse attention over given block lists (the kernel-level entry):
  *   out[b,h,s,:] = softmax_j(sm_scale * q[s].k[j]) v[j]
  * over every key j in the blocks idx[b,h,block_of(s),0..top_k-1].
  * Entries < 0 or >= nb are skipped (padding); a row with no valid block
  * gets zeros.  Duplicate entries are attended once per occurrence (the
  * reference kernels' behaviour).  idx is a dense [B,H,nb,top_k] int32.
+ * order (nullable) is a per-head permutation of the q-blocks giving the
+ * launch order (lcv_bsa_schedule); null launches in block order.
  * Blocks must hold 64 tokens.  D in {16,32,64,128,256} (MFMA path for
  * fp16/bf16 with D in {64,128}; other combinations use a vector-ALU path).
  * Replaces bsa_attention_metal_v4 / _v3 / _v2 / bsa_attention_metal,
@@ -126,20 +139,22 @@ int lcv_bsa_select(const float* qbar, const float* kbar, int64_t B, int64_t H,
 int lcv_bsa_attn_fwd(const void* q, const void* k, const void* v, int dtype,
                      int64_t B, int64_t H, int64_t S, int64_t D,
                      lcv_bsa_strides qs, lcv_bsa_strides ks,
-                     lcv_bsa_strides vs, const int32_t* idx, int64_t top_k,
-                     float sm_scale, lcv_bsa_geom g, void* out,
-                     lcv_bsa_strides os, void* stream);
+                     lcv_bsa_strides vs, const int32_t* idx,
+                     const int32_t* order, int64_t top_k, float sm_scale,
+                     lcv_bsa_geom g, void* out, lcv_bsa_strides os,
+                     void* stream);
 
 /*
- * Bytes of fp32 workspace lcv_bsa_forward needs: the pooled means of q and
- * k, 2*B*H*nb*D*4 bytes.  Host only.
+ * Bytes of workspace lcv_bsa_forward needs: the fp32 pooled means of q and
+ * k (2*B*H*nb*D*4 bytes) and the int32 launch order (B*H*nb*4 bytes), each
+ * rounded up to 256 bytes.  Host only.
  */
 size_t lcv_bsa_forward_workspace_bytes(int64_t B, int64_t H, int64_t nb,
                                        int64_t D);
 
 /*
  * End-to-end block sparse attention: pool q and k, route (scores + top-k),
- * then sparse attention.  idx receives the [B,H,nb,top_k] routing
+ * schedule, then sparse attention.  idx receives the [B,H,nb,top_k] routing
  * (ascending per row); workspace holds at least
  * lcv_bsa_forward_workspace_bytes() bytes, 256-byte aligned.
  * Replaces bsa_attention, block_sparse_attention.py:201-250, whose result

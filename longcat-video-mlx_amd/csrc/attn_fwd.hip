@@ -10,33 +10,55 @@
 // longcat_video/models/block_sparse_attention_metal.py:75-164, 572-712, 829-962)
 // gives the same result.
 //
-// MFMA kernel (fp16 / bf16, D in {64, 128}):
+// MFMA kernel (fp16 / bf16, D in {64, 128}, sm_scale >= 0):
 //   * one workgroup (2 waves) per (b, h, q-block); wave w owns query rows
-//     32w..32w+31 of the block;
+//     32w..32w+31 of the block; two waves per SIMD are resident (register
+//     budget 256), so one wave's softmax overlaps the other's MFMAs;
 //   * the wave's Q tile stays in registers as the B operand of
 //     S^T = K Q^T (v_mfma_f32_32x32x16_{f16,bf16}, fp32 accumulate);
-//   * S^T's accumulator layout (lane = query column, 16 keys per tile) is
-//     exactly the B-operand layout of O^T = V^T P^T once the key order inside
-//     each 16-key step is relabelled, so P never leaves registers and every
-//     lane owns one query row: the online-softmax max/sum need a single
-//     cross-lane exchange (lane ^ 32) and the O rescale is lane-local;
-//   * K is staged in LDS row-major (row stride D+8 halves), V transposed
-//     (V^T, row stride 64+8 halves) with key bits 2 and 3 swapped, which puts
-//     the 8 keys a lane feeds to one MFMA step at adjacent addresses -- every
-//     LDS operand read is one conflict-free 16-byte ds_read;
-//   * the next selected block is fetched into registers while the current one
-//     is multiplied (register double buffering), and workgroups are ordered
-//     so each XCD sweeps the q-blocks of one head (shared K/V in its L2).
+//   * S^T's accumulator layout (lane = query column; runs of 4 consecutive
+//     keys) is the B-operand layout of O^T = V^T P^T, so P never leaves
+//     registers and every lane owns one query row: the online-softmax max/sum
+//     need one cross-lane exchange (lane ^ 32) and the O rescale is lane-local;
+//   * the running max is raised only when a row's tile max exceeds it by more
+//     than 2^8 (a wave-uniform branch), so the O rescale runs on few tiles;
+//     P = exp2(s*scale*log2e - m) <= 256 and its fp16/bf16 copy feeds both
+//     the PV product and the row sum (v_dot2), so numerator and denominator
+//     stay consistent;
+//   * K and V tiles go from HBM straight into LDS with buffer_load ... lds
+//     (no register staging), row-major with 16-byte chunks XOR-swizzled by
+//     row so that every operand read is bank-conflict free: K rows are read
+//     with ds_read_b128, V^T operands with ds_read_b64_tr_b16 (lane L of a
+//     16-lane group receives element L%4 of the rows read by lanes
+//     L/4 + {0,4,8,12}, i.e. 4 consecutive keys of one V column);
+//   * K(j+1) is fetched while tile j's softmax and PV run, V(j+1) while
+//     tile j+1's QK^T runs (single-buffered K and V, explicit vmcnt waits);
+//     workgroups are ordered so each XCD sweeps the q-blocks of one head
+//     (shared K/V in its L2);
+//   * the output tile is staged through LDS and written as whole rows.
 //
-// Vector-ALU kernel (any dtype, D in {16, 32, 64, 128, 256}): 64 rows x 4
-// lanes per workgroup, fp32 throughout; used for fp32 inputs and head dims
-// without an MFMA tiling.
+// Vector-ALU kernel (any dtype, D in {16, 32, 64, 128, 256}, any scale): 64
+// rows x 4 lanes per workgroup, fp32 throughout; used for fp32 inputs, head
+// dims without an MFMA tiling and negative scales.
 #include "bsa_common.h"
 
 namespace lcv {
 namespace {
 
+// Running-max slack of the lazy online softmax, in log2 units.
+constexpr float kRescaleSlack = 8.0f;
+constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit dwords (gfx9 family)
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// NaN-propagating max of three (v_maximum3_f32).
+__device__ __forceinline__ float fmax3(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
 
 __device__ __forceinline__ int next_valid(const int32_t* list, int j, int top_k, int nb) {
   while (j < top_k) {
@@ -47,10 +69,48 @@ __device__ __forceinline__ int next_valid(const int32_t* list, int j, int top_k,
   return j;
 }
 
-// Position of key `key` (0..63) inside a 16-key MFMA step of the V^T tile:
-// swap bits 2 and 3.
-__device__ __forceinline__ int vt_pos(int key) {
-  return (key & ~0xC) | ((key & 0x4) << 1) | ((key & 0x8) >> 1);
+// A q-block's routing list read 64 entries at a time into one register
+// (lane l holds entry base + l); entries come out with v_readlane, so the
+// tile loop issues no vector loads of its own between tile fetches.
+struct BlockList {
+  const int32_t* list;
+  int top_k, nb, base, val;
+  __device__ BlockList(const int32_t* l, int k, int n) : list(l), top_k(k), nb(n), base(0) {
+    val = lane_id() < k ? l[lane_id()] : -1;
+  }
+  __device__ int entry(int j) {  // j uniform, non-decreasing across calls
+    if (j - base >= 64) {
+      base = j & ~63;
+      val = base + lane_id() < top_k ? list[base + lane_id()] : -1;
+    }
+    return __builtin_amdgcn_readlane(val, j - base);
+  }
+  __device__ int next_valid(int j) {  // first j' >= j with a block in [0, nb)
+    while (j < top_k) {
+      const int n = entry(j);
+      if (n >= 0 && n < nb) break;
+      ++j;
+    }
+    return j;
+  }
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// 16 bytes per lane from a raw buffer straight into LDS: lane i writes
+// lds_dst + 16 i (1 KB per wave).  Issued as inline asm so that the only
+// waits on it are the explicit wait_vmcnt<> calls (the compiler otherwise
+// waits for every outstanding LDS load before any LDS read).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, int32_t soffset,
+                                      const void* lds_dst) {
+  const uint32_t m0v = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+               ::"v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(m0v)
+               : "memory");
 }
 
 template <typename T>
@@ -59,40 +119,70 @@ struct Mfma;
 template <>
 struct Mfma<f16> {
   typedef f16x8 vec8;
+  typedef _Float16 vec2 __attribute__((ext_vector_type(2)));
   __device__ static f32x16 mma(vec8 a, vec8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  // Sum of the 8 elements of v added to acc.
+  __device__ static float sum8(vec8 v, float acc) {
+    const vec2 one = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const vec2 pr = {v[2 * i], v[2 * i + 1]};
+      acc = __builtin_amdgcn_fdot2(pr, one, acc, false);
+    }
+    return acc;
   }
 };
 
 template <>
 struct Mfma<bf16> {
   typedef bf16x8 vec8;
+  typedef __bf16 vec2 __attribute__((ext_vector_type(2)));
   __device__ static f32x16 mma(vec8 a, vec8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
+  __device__ static float sum8(vec8 v, float acc) {
+    const vec2 one = {(bf16)1.0f, (bf16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const vec2 pr = {v[2 * i], v[2 * i + 1]};
+      acc = __builtin_amdgcn_fdot2_f32_bf16(pr, one, acc, false);
+    }
+    return acc;
+  }
 };
 
+// Tile geometry.  A K or V tile is 64 rows x D elements, row-major, 2*D
+// bytes per row, DC = D/8 16-byte chunks per row.  Chunk c of row r is stored
+// at chunk position c ^ swz(r):
+//   K: swz = (r / RP) % DC          -- 16 rows read one chunk column: conflict free
+//   V: swz = 4 * ((r / RP) % (DC/4)) -- 4 rows x 4 chunks per 32-lane tr-read: conflict free
+// where RP = 256 / (2*D) rows share one 256-byte bank span.
 template <typename T, int D>
 struct MfmaCfg {
   static constexpr int kThreads = 128;
-  static constexpr int KS = D + 8;         // K tile row stride (elements)
-  static constexpr int VS = 64 + 8;        // V^T tile row stride (elements)
-  static constexpr int DC = D / 8;         // 16-byte chunks per row
-  static constexpr int kPieces = 64 * DC / kThreads;  // K 16-byte loads / thread
-  static constexpr int vItems = 16 * DC / kThreads;   // V (4 keys x 8 d) items / thread
-  static_assert(kPieces >= 1 && vItems >= 1, "tile too small for the workgroup");
+  static constexpr int DC = D / 8;
+  static constexpr int RP = 256 / (2 * D);
+  static constexpr int kRowsPerDma = 64 / DC;              // rows per 1 KB wave load
+  static constexpr int kDmaPerWave = 64 / kRowsPerDma / 2; // loads per wave per tile
+  static constexpr int kTileBytes = 64 * 2 * D;
+  static_assert(D == 64 || D == 128, "MFMA tiling covers D = 64, 128");
+  __device__ static int kswz(int r) { return (r / RP) % DC; }
+  __device__ static int vswz(int r) { return 4 * ((r / RP) % (DC / 4)); }
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(128) void attn_mfma_kernel(AttnParams p) {
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_mfma_kernel(AttnParams p) {
   typedef MfmaCfg<T, D> C;
   typedef typename Mfma<T>::vec8 vec8;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[64 * C::KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[D * C::VS];
+  __shared__ __attribute__((aligned(1024))) uint8_t Ks[C::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t Vs[C::kTileBytes];
 
   const int wid = xcd_linear_work_id(blockIdx.x, gridDim.x);
   const int bh = wid / p.nb;
-  const int qb = wid - bh * p.nb;
+  const int qb = p.order ? uniform_i32(p.order[wid]) : wid - bh * p.nb;
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int tid = threadIdx.x;
@@ -105,6 +195,10 @@ __global__ __launch_bounds__(128) void attn_mfma_kernel(AttnParams p) {
   const T* kbase = reinterpret_cast<const T*>(p.k) + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
   const T* vbase = reinterpret_cast<const T*>(p.v) + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
   T* obase = reinterpret_cast<T*>(p.out) + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh;
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, (int)p.k_head_bytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, (int)p.v_head_bytes, kBufferFlags);
 
   // ---- Q tile: B operand of S^T = K Q^T; lane holds Q[row][16ks + 8g .. +8].
   const int32_t qtok = block_base_token(p.g, qb) + voxel_row_offset(p.g, 32 * wave + l32);
@@ -116,86 +210,67 @@ __global__ __launch_bounds__(128) void attn_mfma_kernel(AttnParams p) {
       qf[ks] = __builtin_bit_cast(vec8, *reinterpret_cast<const u32x4*>(qrow + 16 * ks));
   }
 
-  // ---- Fixed per-thread staging coordinates.
-  int32_t koff[C::kPieces];
-  int kcol[C::kPieces];
-  int klds[C::kPieces];
+  // ---- Direct-to-LDS loads: wave load t fills LDS bytes [1024 t, 1024 t + 1024)
+  // = rows t*RPD .. +RPD; lane i writes chunk position i % DC of row
+  // t*RPD + i / DC and so fetches chunk (i % DC) ^ swz(row) of that row.
+  uint32_t kvo[C::kDmaPerWave], vvo[C::kDmaPerWave];
 #pragma unroll
-  for (int it = 0; it < C::kPieces; ++it) {
-    const int pidx = tid + C::kThreads * it;
-    const int row = pidx / C::DC;
-    const int c = pidx % C::DC;
-    koff[it] = voxel_row_offset(p.g, row);
-    kcol[it] = 8 * c;
-    klds[it] = row * C::KS + 8 * c;
+  for (int u = 0; u < C::kDmaPerWave; ++u) {
+    const int t = wave * C::kDmaPerWave + u;
+    const int row = t * C::kRowsPerDma + lane / C::DC;
+    const int pos = lane % C::DC;
+    const uint32_t tokoff = (uint32_t)voxel_row_offset(p.g, row);
+    kvo[u] = (tokoff * (uint32_t)p.k_ss + 8u * (pos ^ C::kswz(row))) * sizeof(T);
+    vvo[u] = (tokoff * (uint32_t)p.v_ss + 8u * (pos ^ C::vswz(row))) * sizeof(T);
   }
-  int32_t voff[C::vItems][4];
-  int vcol[C::vItems];
-  int vlds[C::vItems];
+  const uint32_t k_row_bytes = (uint32_t)p.k_ss * sizeof(T);
+  const uint32_t v_row_bytes = (uint32_t)p.v_ss * sizeof(T);
+  auto dma_k = [&](int n) {
+    const int off = (int)((uint32_t)uniform_i32(block_base_token(p.g, n)) * k_row_bytes);
 #pragma unroll
-  for (int it = 0; it < C::vItems; ++it) {
-    const int pidx = tid + C::kThreads * it;
-    const int a4 = pidx % 16;  // key quad
-    const int c = pidx / 16;   // d chunk
+    for (int u = 0; u < C::kDmaPerWave; ++u)
+      dma16(krs, kvo[u], off, Ks + 1024 * (wave * C::kDmaPerWave + u));
+  };
+  auto dma_v = [&](int n) {
+    const int off = (int)((uint32_t)uniform_i32(block_base_token(p.g, n)) * v_row_bytes);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) voff[it][r] = voxel_row_offset(p.g, 4 * a4 + r);
-    vcol[it] = 8 * c;
-    vlds[it] = (8 * c) * C::VS + vt_pos(4 * a4);
-  }
+    for (int u = 0; u < C::kDmaPerWave; ++u)
+      dma16(vrs, vvo[u], off, Vs + 1024 * (wave * C::kDmaPerWave + u));
+  };
 
-  u32x4 kreg[C::kPieces];
-  u32x4 vreg[C::vItems][4];
-  auto load_tile = [&](int n) {
-    const int32_t tok0 = block_base_token(p.g, n);
+  // ---- Per-lane LDS read addresses (bytes).
+  // K operand (GEMM1): row 32mt + l32, chunk 2ks + g.
+  int kaddr[2];
 #pragma unroll
-    for (int it = 0; it < C::kPieces; ++it)
-      kreg[it] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)(tok0 + koff[it]) * p.k_ss + kcol[it]);
-#pragma unroll
-    for (int it = 0; it < C::vItems; ++it)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        vreg[it][r] =
-            *reinterpret_cast<const u32x4*>(vbase + (int64_t)(tok0 + voff[it][r]) * p.v_ss + vcol[it]);
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int it = 0; it < C::kPieces; ++it) *reinterpret_cast<u32x4*>(&Ks[klds[it]]) = kreg[it];
-#pragma unroll
-    for (int it = 0; it < C::vItems; ++it) {
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {  // 32-bit word m = elements 2m, 2m+1 of each row
-        const uint32_t w0 = vreg[it][0][m], w1 = vreg[it][1][m];
-        const uint32_t w2 = vreg[it][2][m], w3 = vreg[it][3][m];
-        u32x2 lo, hi;
-        lo[0] = (w0 & 0xffffu) | (w1 << 16);
-        lo[1] = (w2 & 0xffffu) | (w3 << 16);
-        hi[0] = (w0 >> 16) | (w1 & 0xffff0000u);
-        hi[1] = (w2 >> 16) | (w3 & 0xffff0000u);
-        *reinterpret_cast<u32x2*>(&Vt[vlds[it] + (2 * m) * C::VS]) = lo;
-        *reinterpret_cast<u32x2*>(&Vt[vlds[it] + (2 * m + 1) * C::VS]) = hi;
-      }
-    }
-  };
+  for (int mt = 0; mt < 2; ++mt) kaddr[mt] = (32 * mt + l32) * (2 * D);
+  const int ksw0 = C::kswz(l32);  // same swizzle for rows l32 and 32 + l32
+  // V^T operand (GEMM2), step s, half hh, d-tile md: lane i of 16-lane group G
+  // supplies row 16s + 8hh + 4g + i/4, columns 32md + 16(G%2) + 4(i%4) .. +3.
+  const int G = lane / 16, gi = lane % 16;
+  const int vrow0 = 4 * g + gi / 4;                       // + 16s + 8hh
+  const int vcol0 = 16 * (G % 2) + 4 * (gi % 4);           // + 32md (elements)
 
   f32x16 oacc[D / 32];
 #pragma unroll
   for (int md = 0; md < D / 32; ++md)
 #pragma unroll
     for (int i = 0; i < 16; ++i) oacc[md][i] = 0.0f;
-  float m_run = -__builtin_inff();
-  float l_run = 0.0f;
-  const float sl2 = p.scale_log2;
+  float m_run = -__builtin_inff();  // running max of s*scale*log2e (this row)
+  float l_run = 0.0f;               // this lane's partial row sum
+  const float sl2 = p.scale_log2;   // >= 0 on this path
 
-  const int32_t* list = p.idx + ((int64_t)bh * p.nb + qb) * p.top_k;
-  int j = next_valid(list, 0, p.top_k, p.nb);
-  if (j < p.top_k) load_tile(uniform_i32(list[j]));
-
+  BlockList list(p.idx + ((int64_t)bh * p.nb + qb) * p.top_k, p.top_k, p.nb);
+  int j = list.next_valid(0);
+  if (j < p.top_k) {
+    dma_k(list.entry(j));
+    dma_v(list.entry(j));
+  }
   while (j < p.top_k) {
-    __syncthreads();  // every wave is done with the previous tile
-    store_tile();
-    __syncthreads();  // tile visible
-    const int jn = next_valid(list, j + 1, p.top_k, p.nb);
-    if (jn < p.top_k) load_tile(uniform_i32(list[jn]));  // in flight during the math
+    const int jn = list.next_valid(j + 1);
+    const int njn = jn < p.top_k ? list.entry(jn) : 0;
+    // In flight (oldest first): K(j), V(j).
+    wait_vmcnt<C::kDmaPerWave>();
+    __syncthreads();  // K(j) in LDS for both waves
 
     // S^T (64 keys x 32 queries) = K Q^T.
     f32x16 sacc[2];
@@ -207,74 +282,113 @@ __global__ __launch_bounds__(128) void attn_mfma_kernel(AttnParams p) {
     for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
+        const int pos = (2 * ks + g) ^ ksw0;
         const vec8 kf = __builtin_bit_cast(
-            vec8, *reinterpret_cast<const u32x4*>(&Ks[(32 * mt + l32) * C::KS + 16 * ks + 8 * g]));
+            vec8, *reinterpret_cast<const u32x4*>(Ks + kaddr[mt] + 16 * pos));
         sacc[mt] = Mfma<T>::mma(kf, qf[ks], sacc[mt]);
       }
     }
+    __syncthreads();  // both waves done reading K(j)
+    if (jn < p.top_k) dma_k(njn);  // overlaps softmax + PV
 
     // Online softmax for this lane's query row (keys split between g = 0, 1).
-    float t[32];
+    float mx = fmax3(sacc[0][0], sacc[1][0], sacc[0][1]);
+    mx = fmax3(mx, sacc[1][1], sacc[1][1]);
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int i = 2; i < 16; ++i) mx = fmax3(mx, sacc[0][i], sacc[1][i]);
+    mx = fmax3(mx, __shfl_xor(mx, 32), mx) * sl2;
+    if (__ballot(mx > m_run + kRescaleSlack)) {  // wave-uniform
+      const float m_new = fmax3(m_run, mx, mx);
+      const float corr = fast_exp2(m_run - m_new);  // 0 on the first tile
+      l_run *= corr;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) t[16 * mt + i] = sacc[mt][i] * sl2;
-    float mx = t[0];
+      for (int md = 0; md < D / 32; ++md)
 #pragma unroll
-    for (int i = 1; i < 32; ++i) mx = fmaxf(mx, t[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float corr = fast_exp2(m_run - m_new);
-    float psum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      t[i] = fast_exp2(t[i] - m_new);
-      psum += t[i];
+        for (int i = 0; i < 16; ++i) oacc[md][i] *= corr;
+      m_run = m_new;
     }
-    l_run = l_run * corr + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int md = 0; md < D / 32; ++md)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) oacc[md][i] *= corr;
-
-    // P^T as the B operand: step s takes accumulator values 8s .. 8s+7.
+    // P^T as the B operand: step s takes accumulator values 8s .. 8s+7, the
+    // key runs 16s + 4g + {0..3} and 16s + 8 + 4g + {0..3}.
     vec8 pf[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < 4; ++s) {
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) pf[s][jj] = from_f32<T>(t[8 * s + jj]);
+      for (int jj = 0; jj < 8; ++jj) {
+        const int flat = 8 * s + jj;
+        pf[s][jj] = from_f32<T>(fast_exp2(fmaf(sacc[flat / 16][flat % 16], sl2, -m_run)));
+      }
+      l_run = Mfma<T>::sum8(pf[s], l_run);
+    }
+
+    // In flight: V(j) [, K(j+1)].
+    if (jn < p.top_k)
+      wait_vmcnt<C::kDmaPerWave>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();  // V(j) in LDS for both waves
 
     // O^T (D x 32 queries) += V^T P^T.
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
 #pragma unroll
       for (int md = 0; md < D / 32; ++md) {
+        v4s half_lo, half_hi;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int row = 16 * s + 8 * hh + vrow0;
+          const int col = 32 * md + vcol0;
+          const int addr = row * (2 * D) + 16 * ((col / 8) ^ C::vswz(row)) + 2 * (col % 8);
+          const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(Vs + addr));
+          if (hh == 0) half_lo = r; else half_hi = r;
+        }
         const vec8 vf = __builtin_bit_cast(
-            vec8, *reinterpret_cast<const u32x4*>(&Vt[(32 * md + l32) * C::VS + 16 * s + 8 * g]));
+            vec8, (short __attribute__((ext_vector_type(8)))){half_lo[0], half_lo[1], half_lo[2],
+                                                              half_lo[3], half_hi[0], half_hi[1],
+                                                              half_hi[2], half_hi[3]});
         oacc[md] = Mfma<T>::mma(vf, pf[s], oacc[md]);
       }
     }
+    __syncthreads();  // both waves done reading V(j)
+    if (jn < p.top_k) dma_v(njn);  // overlaps the next QK^T
     j = jn;
   }
 
-  // ---- Normalise and store: lane owns O[row][32md + 8(i/4) + 4g + (i%4)].
+  // ---- Normalise, stage the 64 x D output tile in LDS (K tile layout), then
+  // write whole rows: lane owns O[row][32md + 8(i/4) + 4g + (i%4)].
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  T* orow = obase + (int64_t)qtok * p.o_ss;
+  {
+    const int row = 32 * wave + l32;
+    uint8_t* orow = Ks + row * (2 * D);
 #pragma unroll
-  for (int md = 0; md < D / 32; ++md) {
+    for (int md = 0; md < D / 32; ++md) {
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      u32x2 w;
-      w[0] = bits16(from_f32<T>(oacc[md][4 * i4 + 0] * inv)) |
-             (bits16(from_f32<T>(oacc[md][4 * i4 + 1] * inv)) << 16);
-      w[1] = bits16(from_f32<T>(oacc[md][4 * i4 + 2] * inv)) |
-             (bits16(from_f32<T>(oacc[md][4 * i4 + 3] * inv)) << 16);
-      *reinterpret_cast<u32x2*>(orow + 32 * md + 8 * i4 + 4 * g) = w;
+      for (int i4 = 0; i4 < 4; ++i4) {
+        u32x2 w;
+        w[0] = bits16(from_f32<T>(oacc[md][4 * i4 + 0] * inv)) |
+               (bits16(from_f32<T>(oacc[md][4 * i4 + 1] * inv)) << 16);
+        w[1] = bits16(from_f32<T>(oacc[md][4 * i4 + 2] * inv)) |
+               (bits16(from_f32<T>(oacc[md][4 * i4 + 3] * inv)) << 16);
+        const int chunk = 4 * md + i4;
+        *reinterpret_cast<u32x2*>(orow + 16 * (chunk ^ C::kswz(row)) + 8 * g) = w;
+      }
+    }
+  }
+  __syncthreads();
+  {
+    const int32_t tok0 = block_base_token(p.g, qb);
+#pragma unroll
+    for (int u = 0; u < 64 * C::DC / C::kThreads; ++u) {
+      const int pidx = tid + C::kThreads * u;
+      const int row = pidx / C::DC;
+      const int c = pidx % C::DC;
+      const int32_t tok = tok0 + voxel_row_offset(p.g, row);
+      *reinterpret_cast<u32x4*>(obase + (int64_t)tok * p.o_ss + 8 * c) =
+          *reinterpret_cast<const u32x4*>(Ks + row * (2 * D) + 16 * (c ^ C::kswz(row)));
     }
   }
 }
+
 
 // ---------------------------------------------------------------------------
 // Vector-ALU kernel: workgroup = 64 query rows x 4 lanes; lane (r, quarter)
@@ -289,7 +403,7 @@ __global__ __launch_bounds__(256) void attn_valu_kernel(AttnParams p) {
 
   const int wid = xcd_linear_work_id(blockIdx.x, gridDim.x);
   const int bh = wid / p.nb;
-  const int qb = wid - bh * p.nb;
+  const int qb = p.order ? uniform_i32(p.order[wid]) : wid - bh * p.nb;
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int tid = threadIdx.x;
@@ -397,7 +511,7 @@ bool attn_supported(int dtype, int D) {
 }
 
 hipError_t launch_attn(const AttnParams& p, int dtype, int D, hipStream_t stream) {
-  if (attn_uses_mfma(dtype, D)) {
+  if (attn_uses_mfma(dtype, D) && p.scale_log2 >= 0.0f) {
     if (dtype == LCV_BSA_F16)
       return D == 64 ? launch_mfma<f16, 64>(p, stream) : launch_mfma<f16, 128>(p, stream);
     return D == 64 ? launch_mfma<bf16, 64>(p, stream) : launch_mfma<bf16, 128>(p, stream);

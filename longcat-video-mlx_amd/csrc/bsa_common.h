@@ -156,16 +156,24 @@ struct AttnParams {
   int64_t v_sb, v_sh, v_ss;
   int64_t o_sb, o_sh, o_ss;
   const int32_t* idx;
+  const int32_t* order;  // [B*H*nb] launch order of q-blocks per head, or null
   int32_t B, H, nb, top_k;
   float scale_log2;
+  // Bytes spanned by one head of k / v (buffer-descriptor extents).
+  uint32_t k_head_bytes, v_head_bytes;
   Geom g;
 };
 
-// Chooses the MFMA kernel (fp16/bf16, D in {64,128}) or the vector-ALU
-// kernel (any dtype, D in {16,32,64,128,256}).
+// Chooses the MFMA kernel (fp16/bf16, D in {64,128}, scale >= 0) or the
+// vector-ALU kernel (any dtype, D in {16,32,64,128,256}).
 hipError_t launch_attn(const AttnParams& p, int dtype, int D, hipStream_t stream);
 bool attn_supported(int dtype, int D);
 bool attn_uses_mfma(int dtype, int D);
+
+// Per-head q-block launch order from the routing lists (nq <= 4096).
+hipError_t launch_schedule(const int32_t* idx, int BH, int nq, int top_k, int32_t* order,
+                           hipStream_t stream);
+bool schedule_supported(int nq);
 
 hipError_t launch_token_blocks(const Geom& g, int T, int32_t* out, hipStream_t stream);
 hipError_t launch_pair_mask(const int32_t* idx, int B, int H, int nq, int top_k,

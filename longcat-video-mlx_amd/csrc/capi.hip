@@ -8,6 +8,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "bsa_common.h"
@@ -84,6 +85,11 @@ bool vec_aligned(const void* p, const lcv_bsa_strides& s, int vec) {
   return ((uintptr_t)p & 15u) == 0 && s.b % vec == 0 && s.h % vec == 0 && s.s % vec == 0;
 }
 
+// Bytes from the first to one past the last element of one head.
+uint64_t head_bytes(int64_t S, int64_t row_stride, int64_t D, int dtype) {
+  return (uint64_t)((S - 1) * row_stride + D) * (uint64_t)elem_bytes(dtype);
+}
+
 int check_attn_args(const void* q, const void* k, const void* v, const void* out, int dtype,
                     int64_t B, int64_t H, int64_t S, int64_t D, const lcv_bsa_strides& qs,
                     const lcv_bsa_strides& ks, const lcv_bsa_strides& vs,
@@ -109,10 +115,12 @@ int check_attn_args(const void* q, const void* k, const void* v, const void* out
   if (lcv::attn_uses_mfma(dtype, (int)D)) {
     const int vec = 16 / elem_bytes(dtype);
     if (!vec_aligned(q, qs, vec) || !vec_aligned(k, ks, vec) || !vec_aligned(v, vs, vec) ||
-        ((uintptr_t)out & 7u) || os.b % 4 || os.h % 4 || os.s % 4)
+        !vec_aligned(out, os, vec))
       return fail(LCV_BSA_ERR_LAYOUT,
-                  "q/k/v rows must start on 16-byte boundaries and out rows on 8-byte "
-                  "boundaries (strides multiples of 8 / 4 elements)");
+                  "q/k/v/out rows must start on 16-byte boundaries (pointers 16-byte aligned, "
+                  "strides multiples of %d elements)", vec);
+    if (head_bytes(S, ks.s, D, dtype) > 0xFFFFFFFFull || head_bytes(S, vs.s, D, dtype) > 0xFFFFFFFFull)
+      return fail(LCV_BSA_ERR_LAYOUT, "one head of k or v spans more than 4 GiB");
   }
   return LCV_BSA_OK;
 }
@@ -120,8 +128,9 @@ int check_attn_args(const void* q, const void* k, const void* v, const void* out
 lcv::AttnParams make_attn_params(const void* q, const void* k, const void* v, void* out,
                                  const lcv_bsa_strides& qs, const lcv_bsa_strides& ks,
                                  const lcv_bsa_strides& vs, const lcv_bsa_strides& os,
-                                 const int32_t* idx, int64_t B, int64_t H, int64_t nb,
-                                 int64_t top_k, float sm_scale, const lcv_bsa_geom& g) {
+                                 const int32_t* idx, const int32_t* order, int64_t B, int64_t H,
+                                 int64_t S, int64_t D, int dtype, int64_t nb, int64_t top_k,
+                                 float sm_scale, const lcv_bsa_geom& g) {
   lcv::AttnParams p{};
   p.q = q;
   p.k = k;
@@ -132,11 +141,15 @@ lcv::AttnParams make_attn_params(const void* q, const void* k, const void* v, vo
   p.v_sb = vs.b, p.v_sh = vs.h, p.v_ss = vs.s;
   p.o_sb = os.b, p.o_sh = os.h, p.o_ss = os.s;
   p.idx = idx;
+  p.order = order;
   p.B = (int32_t)B;
   p.H = (int32_t)H;
   p.nb = (int32_t)nb;
   p.top_k = (int32_t)top_k;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
+  const uint64_t kb = head_bytes(S, ks.s, D, dtype), vb = head_bytes(S, vs.s, D, dtype);
+  p.k_head_bytes = kb > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)kb;
+  p.v_head_bytes = vb > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)vb;
   p.g = lcv::make_geom(g);
   return p;
 }
@@ -225,26 +238,45 @@ int lcv_bsa_select(const float* qbar, const float* kbar, int64_t B, int64_t H, i
                        "lcv_bsa_select");
 }
 
+int lcv_bsa_schedule(const int32_t* idx, int64_t B, int64_t H, int64_t nq, int64_t top_k,
+                     int32_t* order, void* stream) {
+  if (!idx || !order) return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
+  if (B <= 0 || H <= 0 || nq <= 0 || top_k <= 0)
+    return fail(LCV_BSA_ERR_INVALID_ARG, "B, H, nq, top_k must be positive");
+  if (!lcv::schedule_supported((int)std::min<int64_t>(nq, kI32Max)) || B * H > kI32Max ||
+      B * H * nq * top_k > ((int64_t)1 << 40))
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "scheduling supports nq <= 4096 (got %lld)", (long long)nq);
+  return launch_status(lcv::launch_schedule(idx, (int)(B * H), (int)nq, (int)top_k, order,
+                                            (hipStream_t)stream),
+                       "lcv_bsa_schedule");
+}
+
 int lcv_bsa_attn_fwd(const void* q, const void* k, const void* v, int dtype, int64_t B,
                      int64_t H, int64_t S, int64_t D, lcv_bsa_strides qs, lcv_bsa_strides ks,
-                     lcv_bsa_strides vs, const int32_t* idx, int64_t top_k, float sm_scale,
-                     lcv_bsa_geom g, void* out, lcv_bsa_strides os, void* stream) {
+                     lcv_bsa_strides vs, const int32_t* idx, const int32_t* order, int64_t top_k,
+                     float sm_scale, lcv_bsa_geom g, void* out, lcv_bsa_strides os,
+                     void* stream) {
   int64_t nb = 0, bs = 0;
   int st = check_attn_args(q, k, v, out, dtype, B, H, S, D, qs, ks, vs, os, top_k, sm_scale, g,
                            &nb, &bs);
   if (st) return st;
   if (!idx) return fail(LCV_BSA_ERR_INVALID_ARG, "null block index pointer");
-  const lcv::AttnParams p =
-      make_attn_params(q, k, v, out, qs, ks, vs, os, idx, B, H, nb, top_k, sm_scale, g);
+  const lcv::AttnParams p = make_attn_params(q, k, v, out, qs, ks, vs, os, idx, order, B, H, S, D,
+                                             dtype, nb, top_k, sm_scale, g);
   return launch_status(lcv::launch_attn(p, dtype, (int)D, (hipStream_t)stream),
                        "lcv_bsa_attn_fwd");
 }
 
+namespace {
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+size_t pooled_bytes(int64_t B, int64_t H, int64_t nb, int64_t D) {
+  return align256((size_t)B * H * nb * D * sizeof(float));
+}
+}  // namespace
+
 size_t lcv_bsa_forward_workspace_bytes(int64_t B, int64_t H, int64_t nb, int64_t D) {
   if (B <= 0 || H <= 0 || nb <= 0 || D <= 0) return 0;
-  const size_t one = (size_t)B * H * nb * D * sizeof(float);
-  const size_t one_aligned = (one + 255) & ~(size_t)255;
-  return 2 * one_aligned;
+  return 2 * pooled_bytes(B, H, nb, D) + align256((size_t)B * H * nb * sizeof(int32_t));
 }
 
 int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
@@ -267,8 +299,10 @@ int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype, int6
                 "workspace must be 256-byte aligned and hold %zu bytes (got %zu)", need,
                 workspace_bytes);
   hipStream_t s = (hipStream_t)stream;
+  const size_t pb = pooled_bytes(B, H, nb, D);
   float* qbar = reinterpret_cast<float*>(workspace);
-  float* kbar = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + need / 2);
+  float* kbar = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + pb);
+  int32_t* order = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + 2 * pb);
   const lcv::Tensor4 ts[2] = {{q, qs.b, qs.h, qs.s}, {k, ks.b, ks.h, ks.s}};
   float* outs[2] = {qbar, kbar};
   const lcv::Geom gg = lcv::make_geom(g);
@@ -280,8 +314,15 @@ int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype, int6
                                         (int)top_k, idx, s),
                      "lcv_bsa_forward(select)");
   if (st) return st;
-  const lcv::AttnParams p =
-      make_attn_params(q, k, v, out, qs, ks, vs, os, idx, B, H, nb, top_k, sm_scale, g);
+  const bool sched = lcv::schedule_supported((int)nb);
+  if (sched) {
+    st = launch_status(lcv::launch_schedule(idx, (int)(B * H), (int)nb, (int)top_k, order, s),
+                       "lcv_bsa_forward(schedule)");
+    if (st) return st;
+  }
+  const lcv::AttnParams p = make_attn_params(q, k, v, out, qs, ks, vs, os, idx,
+                                             sched ? order : nullptr, B, H, S, D, dtype, nb,
+                                             top_k, sm_scale, g);
   return launch_status(lcv::launch_attn(p, dtype, (int)D, s), "lcv_bsa_forward(attn)");
 }
 

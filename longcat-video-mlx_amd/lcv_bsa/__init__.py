@@ -20,6 +20,7 @@ from .block_sparse_attention import (  # noqa: F401
 )
 from .block_sparse_attention_hip import (  # noqa: F401
     bsa_attention_hip,
+    schedule_block_order,
     reshape_from_block_major,
     reshape_to_block_major,
 )

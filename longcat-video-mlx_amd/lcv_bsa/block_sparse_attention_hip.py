@@ -23,7 +23,29 @@ from .block_sparse_attention import (
     num_blocks,
 )
 
-__all__ = ["bsa_attention_hip", "reshape_to_block_major", "reshape_from_block_major"]
+__all__ = [
+    "bsa_attention_hip", "schedule_block_order", "reshape_to_block_major",
+    "reshape_from_block_major",
+]
+
+MAX_SCHEDULED_BLOCKS = 4096
+
+
+def schedule_block_order(block_indices: torch.Tensor) -> torch.Tensor:
+    """Per-head launch order of the q-blocks (``[B, H, nq]`` int32 permutation).
+
+    q-blocks are sorted by the first and middle entries of their routing
+    lists, so that blocks whose ascending lists start together run together
+    and re-use each other's K/V tiles from L2.  Any order gives the same
+    attention output.  nq <= 4096.
+    """
+    _require_device(block_indices)
+    bi = block_indices.to(torch.int32).contiguous()
+    B, H, nq, k = bi.shape
+    order = torch.empty((B, H, nq), dtype=torch.int32, device=bi.device)
+    st = _lib.load().lcv_bsa_schedule(bi.data_ptr(), B, H, nq, k, order.data_ptr(), _stream(bi))
+    _lib.check(st, "schedule_block_order")
+    return order
 
 
 def bsa_attention_hip(
@@ -81,10 +103,12 @@ def bsa_attention_hip(
     code = _dtype_code(q)
     if code != _lib.F32:
         q, k, v = _aligned_rows(q), _aligned_rows(k), _aligned_rows(v)
+    order = schedule_block_order(bi) if nb <= MAX_SCHEDULED_BLOCKS else None
     out = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
     st = _lib.load().lcv_bsa_attn_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), code, B, H, S, D,
-        _strides(q), _strides(k), _strides(v), bi.data_ptr(), top_k, float(sm_scale),
+        _strides(q), _strides(k), _strides(v), bi.data_ptr(),
+        order.data_ptr() if order is not None else None, top_k, float(sm_scale),
         _geom(shape, chunk_thw), out.data_ptr(), _strides(out), _stream(q),
     )
     _lib.check(st, "bsa_attention_hip")

@@ -64,23 +64,23 @@ def test_c_abi_validation_returns_before_launch():
     assert st == _lib.ERR_DTYPE
     args = dict(B=1, H=1, S=64, D=128)
     st = lib.lcv_bsa_attn_fwd(fake, fake, fake, 0, 1, 1, 64, 128, S_(8192, 8192, 128),
-                              S_(8192, 8192, 128), S_(8192, 8192, 128), fake, 0, 0.1,
+                              S_(8192, 8192, 128), S_(8192, 8192, 128), fake, None, 0, 0.1,
                               G(4, 4, 4, 4, 4, 4), fake, S_(8192, 8192, 128), None)
     assert st == _lib.ERR_INVALID_ARG  # top_k = 0
     st = lib.lcv_bsa_attn_fwd(fake, fake, fake, 0, 1, 1, 8, 128, S_(1024, 1024, 128),
-                              S_(1024, 1024, 128), S_(1024, 1024, 128), fake, 1, 0.1,
+                              S_(1024, 1024, 128), S_(1024, 1024, 128), fake, None, 1, 0.1,
                               G(2, 2, 2, 2, 2, 2), fake, S_(1024, 1024, 128), None)
     assert st == _lib.ERR_UNSUPPORTED and b"64-token" in lib.lcv_bsa_last_error()
     st = lib.lcv_bsa_attn_fwd(fake, fake, fake, 0, 1, 1, 64, 24, S_(1536, 1536, 24),
-                              S_(1536, 1536, 24), S_(1536, 1536, 24), fake, 1, 0.1,
+                              S_(1536, 1536, 24), S_(1536, 1536, 24), fake, None, 1, 0.1,
                               G(4, 4, 4, 4, 4, 4), fake, S_(1536, 1536, 24), None)
     assert st == _lib.ERR_UNSUPPORTED and b"head_dim" in lib.lcv_bsa_last_error()
     st = lib.lcv_bsa_attn_fwd(fake + 2, fake, fake, 0, 1, 1, 64, 128, S_(8192, 8192, 128),
-                              S_(8192, 8192, 128), S_(8192, 8192, 128), fake, 1, 0.1,
+                              S_(8192, 8192, 128), S_(8192, 8192, 128), fake, None, 1, 0.1,
                               G(4, 4, 4, 4, 4, 4), fake, S_(8192, 8192, 128), None)
     assert st == _lib.ERR_LAYOUT
     st = lib.lcv_bsa_attn_fwd(fake, fake, fake, 0, 1, 1, 64, 128, S_(8192, 8192, 64),
-                              S_(8192, 8192, 128), S_(8192, 8192, 128), fake, 1, 0.1,
+                              S_(8192, 8192, 128), S_(8192, 8192, 128), fake, None, 1, 0.1,
                               G(4, 4, 4, 4, 4, 4), fake, S_(8192, 8192, 128), None)
     assert st == _lib.ERR_LAYOUT  # row stride below D
     st = lib.lcv_bsa_topk(fake, 1, 1, 4, 8, 9, fake, None)
@@ -90,7 +90,9 @@ def test_c_abi_validation_returns_before_launch():
     st = lib.lcv_bsa_select(fake, fake, 1, 1, 4, 8, 6, 4, fake, None)
     assert st == _lib.ERR_UNSUPPORTED  # D % 4
     ws = lib.lcv_bsa_forward_workspace_bytes(1, 32, 900, 128)
-    assert ws == 2 * 32 * 900 * 128 * 4
+    assert ws == 2 * 32 * 900 * 128 * 4 + (32 * 900 * 4 + 255) // 256 * 256
+    st = lib.lcv_bsa_schedule(fake, 1, 1, 5000, 4, fake, None)
+    assert st == _lib.ERR_UNSUPPORTED  # nq > 4096
     st = lib.lcv_bsa_forward(fake, fake, fake, 0, 1, 1, 4096, 128, S_(1 << 19, 1 << 19, 128),
                              S_(1 << 19, 1 << 19, 128), S_(1 << 19, 1 << 19, 128), 4, 0.1,
                              G(1, 1, 4096, 1, 1, 64), fake, 16, fake, fake,

@@ -319,3 +319,54 @@ def test_block_major_permutation_exact(device, dtype):
     bm = reshape_to_block_major(x, shape, chunk)
     assert np.array_equal(_np(bm), O.reshape_to_block_major(_np(x), shape, chunk))
     assert torch.equal(reshape_from_block_major(bm, shape, chunk), x)
+
+
+# ---------------------------------------------------------------------------
+# Launch order (scheduling): a permutation; results independent of it
+# ---------------------------------------------------------------------------
+
+def _attn_with_order(q, k, v, idx, shape, chunk, order):
+    from lcv_bsa import _lib
+    from lcv_bsa.block_sparse_attention import _geom, _strides
+
+    B, H, S, D = q.shape
+    out = torch.empty_like(q)
+    st = _lib.load().lcv_bsa_attn_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), {torch.float16: 0, torch.bfloat16: 1,
+                                                   torch.float32: 2}[q.dtype],
+        B, H, S, D, _strides(q), _strides(k), _strides(v), idx.data_ptr(),
+        order.data_ptr() if order is not None else None, idx.shape[3], 1.0 / math.sqrt(D),
+        _geom(shape, chunk), out.data_ptr(), _strides(out), torch.cuda.current_stream().cuda_stream)
+    _lib.check(st, "attn")
+    return out
+
+
+@pytest.mark.parametrize("nb,k", [(1, 1), (7, 3), (64, 4), (900, 57), (4096, 5)])
+def test_schedule_permutation_sorted_by_key(device, nb, k):
+    from lcv_bsa import schedule_block_order
+
+    idx = np.sort(_distinct_indices(1, 2, nb, nb, k, seed=nb), axis=-1)
+    if nb >= 7:
+        idx[0, 0, 3, :] = -1  # padding sorts as nb
+    order = schedule_block_order(torch.from_numpy(idx).to(device)).cpu().numpy()
+    for h in range(2):
+        assert sorted(order[0, h].tolist()) == list(range(nb))
+        first = np.where((idx[0, h, :, 0] >= 0), idx[0, h, :, 0], nb)
+        med = np.where((idx[0, h, :, k // 2] >= 0), idx[0, h, :, k // 2], nb)
+        keys = [(first[i], med[i], i) for i in order[0, h]]
+        assert keys == sorted(keys)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_attention_independent_of_order(device, dtype):
+    from lcv_bsa import schedule_block_order
+
+    shape, chunk = (1, 1, 4096), (1, 1, 64)
+    D = 128 if dtype != torch.float32 else 64
+    q, k, v = (_rand((1, 3, 4096, D), dtype, device, seed=s) for s in (21, 22, 23))
+    idx = torch.from_numpy(np.sort(_distinct_indices(1, 3, 64, 64, 9, seed=5), axis=-1)).to(device)
+    base = _attn_with_order(q, k, v, idx, shape, chunk, None)
+    sched = _attn_with_order(q, k, v, idx, shape, chunk, schedule_block_order(idx))
+    rnd = torch.stack([torch.randperm(64) for _ in range(3)])[None].to(torch.int32).to(device)
+    rand = _attn_with_order(q, k, v, idx, shape, chunk, rnd)
+    assert torch.equal(base, sched) and torch.equal(base, rand)
