@@ -208,6 +208,11 @@ void attn_mfma_kernel(AttnParams p) {
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks)
       qf[ks] = __builtin_bit_cast(vec8, *reinterpret_cast<const u32x4*>(qrow + 16 * ks));
+    // Consume the fragments here so the compiler's own vmcnt bookkeeping
+    // retires these loads before the tile loop; inside the loop the only
+    // outstanding vector loads are the tile DMAs, waited on explicitly.
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) asm volatile("" ::"v"(qf[ks]));
   }
 
   // ---- Direct-to-LDS loads: wave load t fills LDS bytes [1024 t, 1024 t + 1024)
@@ -278,15 +283,28 @@ void attn_mfma_kernel(AttnParams p) {
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) sacc[mt][i] = 0.0f;
+    // K operand reads run kPf k-steps ahead of the MFMAs that consume them
+    // (scheduling groups keep the compiler from sinking them back), so the
+    // MFMA chain does not wait on LDS latency.
+    constexpr int kSteps = D / 16;
+    constexpr int kPf = kSteps < 4 ? kSteps : 4;
+    vec8 kf[2][kSteps];
+    auto read_k = [&](int ks) {
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
+      for (int mt = 0; mt < 2; ++mt)
+        kf[mt][ks] = __builtin_bit_cast(
+            vec8, *reinterpret_cast<const u32x4*>(Ks + kaddr[mt] + 16 * ((2 * ks + g) ^ ksw0)));
+    };
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int pos = (2 * ks + g) ^ ksw0;
-        const vec8 kf = __builtin_bit_cast(
-            vec8, *reinterpret_cast<const u32x4*>(Ks + kaddr[mt] + 16 * pos));
-        sacc[mt] = Mfma<T>::mma(kf, qf[ks], sacc[mt]);
-      }
+    for (int ks = 0; ks < kPf; ++ks) read_k(ks);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPf, 0);  // DS reads
+#pragma unroll
+    for (int ks = 0; ks < kSteps; ++ks) {
+      if (ks + kPf < kSteps) read_k(ks + kPf);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) sacc[mt] = Mfma<T>::mma(kf[mt][ks], qf[ks], sacc[mt]);
+      if (ks + kPf < kSteps) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
     }
     __syncthreads();  // both waves done reading K(j)
     if (jn < p.top_k) dma_k(njn);  // overlaps softmax + PV
