@@ -19,7 +19,8 @@
 //   * S^T's accumulator layout (lane = query column; runs of 4 consecutive
 //     keys) is the B-operand layout of O^T = V^T P^T, so P never leaves
 //     registers and every lane owns one query row: the online-softmax max/sum
-//     need one cross-lane exchange (lane ^ 32) and the O rescale is lane-local;
+//     need one cross-lane exchange (lane ^ 32, v_permlane32_swap) and the O
+//     rescale is lane-local;
 //   * the running max is raised only when a row's tile max exceeds it by more
 //     than 2^8 (a wave-uniform branch), so the O rescale runs on few tiles;
 //     P = exp2(s*scale*log2e - m) <= 256 and its fp16/bf16 copy feeds both
@@ -35,6 +36,8 @@
 //     tile j+1's QK^T runs (single-buffered K and V, explicit vmcnt waits);
 //     workgroups are ordered so each XCD sweeps the q-blocks of one head
 //     (shared K/V in its L2);
+//   * the routing list is read 64 entries at a time; each lane turns its entry
+//     into the block's first token once, so a tile costs one v_readlane;
 //   * the output tile is staged through LDS and written as whole rows.
 //
 // Vector-ALU kernel (any dtype, D in {16, 32, 64, 128, 256}, any scale): 64
@@ -60,6 +63,25 @@ __device__ __forceinline__ float fmax3(float a, float b, float c) {
   return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
+// Lanes l and l ^ 32 exchange x through v_permlane32_swap (a VALU op; no
+// LDS round trip); the two results hold x[l] and x[l ^ 32] in some order.
+__device__ __forceinline__ void swap_halves(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                                  __builtin_bit_cast(uint32_t, x), false, false);
+  a = __builtin_bit_cast(float, (uint32_t)r[0]);
+  b = __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+__device__ __forceinline__ float max_halves(float x) {
+  float a, b;
+  swap_halves(x, a, b);
+  return __builtin_elementwise_maximum(a, b);
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  float a, b;
+  swap_halves(x, a, b);
+  return a + b;
+}
+
 __device__ __forceinline__ int next_valid(const int32_t* list, int j, int top_k, int nb) {
   while (j < top_k) {
     const int n = uniform_i32(list[j]);
@@ -69,30 +91,40 @@ __device__ __forceinline__ int next_valid(const int32_t* list, int j, int top_k,
   return j;
 }
 
-// A q-block's routing list read 64 entries at a time into one register
-// (lane l holds entry base + l); entries come out with v_readlane, so the
-// tile loop issues no vector loads of its own between tile fetches.
-struct BlockList {
+// A q-block's routing list, read 64 entries at a time into one register:
+// lane l holds the first token of block list[base + l] (-1 if the entry is
+// outside [0, nb)), computed once per chunk with vector ops, plus a wave mask
+// of the valid entries.  The tile loop then needs one v_readlane per tile
+// and issues no vector loads of its own between tile fetches.
+struct TileList {
   const int32_t* list;
-  int top_k, nb, base, val;
-  __device__ BlockList(const int32_t* l, int k, int n) : list(l), top_k(k), nb(n), base(0) {
-    val = lane_id() < k ? l[lane_id()] : -1;
+  int top_k, nb, base;
+  int tok;         // per lane
+  uint64_t valid;  // bit l: entry base + l is a block in [0, nb)
+  __device__ TileList(const int32_t* l, int k, int n, const Geom& g) : list(l), top_k(k), nb(n) {
+    load(0, g);
   }
-  __device__ int entry(int j) {  // j uniform, non-decreasing across calls
-    if (j - base >= 64) {
-      base = j & ~63;
-      val = base + lane_id() < top_k ? list[base + lane_id()] : -1;
-    }
-    return __builtin_amdgcn_readlane(val, j - base);
+  __device__ void load(int b, const Geom& g) {
+    base = b;
+    const int j = b + lane_id();
+    const int n = j < top_k ? list[j] : -1;
+    const bool ok = n >= 0 && n < nb;
+    tok = ok ? block_base_token(g, n) : -1;
+    valid = __ballot(ok);
   }
-  __device__ int next_valid(int j) {  // first j' >= j with a block in [0, nb)
+  // First j' >= j whose entry is valid, or top_k.  j uniform and
+  // non-decreasing across calls.
+  __device__ int next(int j, const Geom& g) {
     while (j < top_k) {
-      const int n = entry(j);
-      if (n >= 0 && n < nb) break;
-      ++j;
+      if (j - base >= 64) load(j & ~63, g);
+      const uint64_t m = valid >> (j - base);
+      if (m) return j + (int)__builtin_ctzll(m);
+      j = base + 64;
     }
-    return j;
+    return top_k;
   }
+  // First token of entry j (valid, within the current chunk).
+  __device__ int32_t token(int j) const { return __builtin_amdgcn_readlane(tok, j - base); }
 };
 
 template <int N>
@@ -186,7 +218,7 @@ void attn_mfma_kernel(AttnParams p) {
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int tid = threadIdx.x;
-  const int wave = tid / 64;
+  const int wave = uniform_i32(tid / 64);
   const int lane = tid % 64;
   const int l32 = lane % 32;
   const int g = lane / 32;
@@ -230,14 +262,15 @@ void attn_mfma_kernel(AttnParams p) {
   }
   const uint32_t k_row_bytes = (uint32_t)p.k_ss * sizeof(T);
   const uint32_t v_row_bytes = (uint32_t)p.v_ss * sizeof(T);
-  auto dma_k = [&](int n) {
-    const int off = (int)((uint32_t)uniform_i32(block_base_token(p.g, n)) * k_row_bytes);
+  // tok: first token of the block (uniform).
+  auto dma_k = [&](int32_t tok) {
+    const int off = (int)((uint32_t)tok * k_row_bytes);
 #pragma unroll
     for (int u = 0; u < C::kDmaPerWave; ++u)
       dma16(krs, kvo[u], off, Ks + 1024 * (wave * C::kDmaPerWave + u));
   };
-  auto dma_v = [&](int n) {
-    const int off = (int)((uint32_t)uniform_i32(block_base_token(p.g, n)) * v_row_bytes);
+  auto dma_v = [&](int32_t tok) {
+    const int off = (int)((uint32_t)tok * v_row_bytes);
 #pragma unroll
     for (int u = 0; u < C::kDmaPerWave; ++u)
       dma16(vrs, vvo[u], off, Vs + 1024 * (wave * C::kDmaPerWave + u));
@@ -264,15 +297,16 @@ void attn_mfma_kernel(AttnParams p) {
   float l_run = 0.0f;               // this lane's partial row sum
   const float sl2 = p.scale_log2;   // >= 0 on this path
 
-  BlockList list(p.idx + ((int64_t)bh * p.nb + qb) * p.top_k, p.top_k, p.nb);
-  int j = list.next_valid(0);
+  TileList list(p.idx + ((int64_t)bh * p.nb + qb) * p.top_k, p.top_k, p.nb, p.g);
+  int j = list.next(0, p.g);
   if (j < p.top_k) {
-    dma_k(list.entry(j));
-    dma_v(list.entry(j));
+    const int32_t tok = list.token(j);
+    dma_k(tok);
+    dma_v(tok);
   }
   while (j < p.top_k) {
-    const int jn = list.next_valid(j + 1);
-    const int njn = jn < p.top_k ? list.entry(jn) : 0;
+    const int jn = list.next(j + 1, p.g);
+    const int32_t njn = jn < p.top_k ? list.token(jn) : 0;
     // In flight (oldest first): K(j), V(j).
     wait_vmcnt<C::kDmaPerWave>();
     __syncthreads();  // K(j) in LDS for both waves
@@ -314,7 +348,7 @@ void attn_mfma_kernel(AttnParams p) {
     mx = fmax3(mx, sacc[1][1], sacc[1][1]);
 #pragma unroll
     for (int i = 2; i < 16; ++i) mx = fmax3(mx, sacc[0][i], sacc[1][i]);
-    mx = fmax3(mx, __shfl_xor(mx, 32), mx) * sl2;
+    mx = max_halves(mx) * sl2;
     if (__ballot(mx > m_run + kRescaleSlack)) {  // wave-uniform
       const float m_new = fmax3(m_run, mx, mx);
       const float corr = fast_exp2(m_run - m_new);  // 0 on the first tile
@@ -345,25 +379,39 @@ void attn_mfma_kernel(AttnParams p) {
       wait_vmcnt<0>();
     __syncthreads();  // V(j) in LDS for both waves
 
-    // O^T (D x 32 queries) += V^T P^T.
+    // O^T (D x 32 queries) += V^T P^T; V^T fragments of step s + 1 are read
+    // while the MFMAs of step s run.
+    {
+      vec8 vf[4][D / 32];
+      auto read_v = [&](int s) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+        for (int md = 0; md < D / 32; ++md) {
+          v4s half_lo, half_hi;
 #pragma unroll
-      for (int md = 0; md < D / 32; ++md) {
-        v4s half_lo, half_hi;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int row = 16 * s + 8 * hh + vrow0;
-          const int col = 32 * md + vcol0;
-          const int addr = row * (2 * D) + 16 * ((col / 8) ^ C::vswz(row)) + 2 * (col % 8);
-          const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(Vs + addr));
-          if (hh == 0) half_lo = r; else half_hi = r;
+          for (int hh = 0; hh < 2; ++hh) {
+            const int row = 16 * s + 8 * hh + vrow0;
+            const int col = 32 * md + vcol0;
+            const int addr = row * (2 * D) + 16 * ((col / 8) ^ C::vswz(row)) + 2 * (col % 8);
+            const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(Vs + addr));
+            if (hh == 0) half_lo = r; else half_hi = r;
+          }
+          vf[s][md] = __builtin_bit_cast(
+              vec8, (short __attribute__((ext_vector_type(8)))){half_lo[0], half_lo[1], half_lo[2],
+                                                                half_lo[3], half_hi[0], half_hi[1],
+                                                                half_hi[2], half_hi[3]});
         }
-        const vec8 vf = __builtin_bit_cast(
-            vec8, (short __attribute__((ext_vector_type(8)))){half_lo[0], half_lo[1], half_lo[2],
-                                                              half_lo[3], half_hi[0], half_hi[1],
-                                                              half_hi[2], half_hi[3]});
-        oacc[md] = Mfma<T>::mma(vf, pf[s], oacc[md]);
+      };
+      read_v(0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * (D / 32), 0);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (s + 1 < 4) read_v(s + 1);
+#pragma unroll
+        for (int md = 0; md < D / 32; ++md) {
+          oacc[md] = Mfma<T>::mma(vf[s][md], pf[s], oacc[md]);
+          if (s + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
       }
     }
     __syncthreads();  // both waves done reading V(j)
@@ -373,7 +421,7 @@ void attn_mfma_kernel(AttnParams p) {
 
   // ---- Normalise, stage the 64 x D output tile in LDS (K tile layout), then
   // write whole rows: lane owns O[row][32md + 8(i/4) + 4g + (i%4)].
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = sum_halves(l_run);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   {
     const int row = 32 * wave + l32;
