@@ -1,5 +1,9 @@
 // Block routing: fp32 block scores qbar . kbar^T and per-row top-k.
 //
+// The score GEMM runs on fp32 MFMA for head dims 64 and 128 (nk <= 2048) and
+// on fp32 FMAs otherwise; either way each score is an fp32 dot product, and
+// selection is exact given score margins well above fp32 rounding.
+//
 // Follows block_routing_scores + topk_block_indices
 // (longcat_video/models/block_sparse_attention.py:107-134).  The reference
 // materialises the [B,H,nq,nk] score tensor and runs argpartition; here a
@@ -40,14 +44,19 @@ __device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out) 
     key[e] = col < nk ? order_key(sc[e]) : 0u;
   }
   // Largest threshold t with #(key >= t) >= k, built bit by bit.  Padding
-  // columns carry key 0 and never reach a candidate >= 1.
+  // columns carry key 0 and never reach a candidate >= 1.  Once a candidate
+  // has exactly k keys at or above it, those keys are the top k and the
+  // remaining bits cannot change the selection.
   uint32_t thr = 0u;
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t cand = thr | (1u << bit);
     int cnt = 0;
 #pragma unroll
     for (int e = 0; e < NPER; ++e) cnt += __popcll(ballot64(key[e] >= cand));
-    if (cnt >= k) thr = cand;
+    if (cnt >= k) {
+      thr = cand;
+      if (cnt == k) break;
+    }
   }
   int gt = 0;
 #pragma unroll
@@ -178,6 +187,95 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   }
 }
 
+// Score rows on fp32 MFMA (v_mfma_f32_16x16x4_f32).  One workgroup = 16
+// q-block rows of one (b, h); wave w computes the 16-column score tiles
+// w, w + 4, ... .  Operands come straight from global memory into registers:
+// lane (c, kg) (c = lane % 16, kg = lane / 16) holds dims [kg*D/4, (kg+1)*D/4)
+// of q-block row c (A) and of key row 16t + c (B), so k-step s pairs dim
+// kg*D/4 + s of both.  The accumulator holds S[4kg + i][16t + c].  kSelect
+// gathers the 16 x nk rows in LDS and runs wave_topk on them; kScoresOnly
+// writes the tiles to global memory.
+template <int NPER, int MODE, int D>
+__global__ __launch_bounds__(256) void route_mfma_kernel(RouteArgs a) {
+  constexpr int QR = 16;
+  constexpr int DQ = D / 4;                 // dims per lane group
+  constexpr int LDSW = NPER * 64 + 4;       // score row stride (floats)
+  constexpr int kLds = MODE == kSelect ? QR * LDSW : 1;
+  __shared__ __attribute__((aligned(16))) float srow[kLds];
+  const int tid = threadIdx.x;
+  const int wave = tid / 64;
+  const int lane = tid % 64;
+  const int c = lane % 16;
+  const int kg = lane / 16;
+  const int bh = blockIdx.x / a.tiles_per_bh;
+  const int row0 = (blockIdx.x - bh * a.tiles_per_bh) * QR;
+  const float* qb = a.qbar + (int64_t)bh * a.nq * D;
+  const float* kb = a.kbar + (int64_t)bh * a.nk * D;
+
+  float qa[DQ];
+  {
+    const int row = row0 + c;
+#pragma unroll
+    for (int s4 = 0; s4 < DQ / 4; ++s4) {
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (row < a.nq) v = *reinterpret_cast<const f32x4*>(qb + (int64_t)row * D + kg * DQ + 4 * s4);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) qa[4 * s4 + u] = v[u];
+    }
+  }
+  const int ntiles = (a.nk + 15) / 16;
+  auto load_b = [&](int t, float (&kv)[DQ]) {
+    const int key = 16 * t + c;
+#pragma unroll
+    for (int s4 = 0; s4 < DQ / 4; ++s4) {
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (key < a.nk) v = *reinterpret_cast<const f32x4*>(kb + (int64_t)key * D + kg * DQ + 4 * s4);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) kv[4 * s4 + u] = v[u];
+    }
+  };
+  float kv0[DQ], kv1[DQ];
+  int t = wave;
+  if (t < ntiles) load_b(t, kv0);
+  auto tile = [&](int tt, const float (&kv)[DQ]) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < DQ; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], kv[s], acc, 0, 0, 0);
+    const int col = 16 * tt + c;
+    if (MODE == kSelect) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) srow[(4 * kg + i) * LDSW + col] = acc[i];
+    } else {
+      if (col < a.nk) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + 4 * kg + i;
+          if (row < a.nq) a.score_out[((int64_t)bh * a.nq + row) * a.nk + col] = acc[i];
+        }
+      }
+    }
+  };
+  for (; t < ntiles; t += 8) {
+    if (t + 4 < ntiles) load_b(t + 4, kv1);
+    tile(t, kv0);
+    if (t + 4 >= ntiles) break;
+    if (t + 8 < ntiles) load_b(t + 8, kv0);
+    tile(t + 4, kv1);
+  }
+  if (MODE == kSelect) {
+    __syncthreads();
+#pragma unroll 1
+    for (int r = wave; r < QR; r += 4) {
+      const int row = row0 + r;
+      if (row >= a.nq) break;  // wave-uniform; rows only grow
+      float sc[NPER];
+#pragma unroll
+      for (int e = 0; e < NPER; ++e) sc[e] = srow[r * LDSW + e * 64 + lane];
+      wave_topk<NPER>(sc, a.nk, a.top_k, a.idx + ((int64_t)bh * a.nq + row) * a.top_k);
+    }
+  }
+}
+
 template <int NPER, int MODE>
 hipError_t launch_route_n(RouteArgs a, int BH, hipStream_t stream) {
   constexpr int RW = NPER <= 16 ? 4 : (NPER == 32 ? 2 : 1);
@@ -187,9 +285,34 @@ hipError_t launch_route_n(RouteArgs a, int BH, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <int NPER, int MODE, int D>
+hipError_t launch_route_mfma_n(RouteArgs a, int BH, hipStream_t stream) {
+  a.tiles_per_bh = (a.nq + 15) / 16;
+  hipLaunchKernelGGL((route_mfma_kernel<NPER, MODE, D>), dim3(BH * a.tiles_per_bh), dim3(256), 0,
+                     stream, a);
+  return hipGetLastError();
+}
+
+template <int MODE, int D>
+hipError_t launch_route_mfma(RouteArgs a, int BH, hipStream_t stream) {
+  const int per = (a.nk + 63) / 64;
+  if (per <= 1) return launch_route_mfma_n<1, MODE, D>(a, BH, stream);
+  if (per <= 2) return launch_route_mfma_n<2, MODE, D>(a, BH, stream);
+  if (per <= 4) return launch_route_mfma_n<4, MODE, D>(a, BH, stream);
+  if (per <= 8) return launch_route_mfma_n<8, MODE, D>(a, BH, stream);
+  if (per <= 16) return launch_route_mfma_n<16, MODE, D>(a, BH, stream);
+  return launch_route_mfma_n<32, MODE, D>(a, BH, stream);
+}
+
 template <int MODE>
 hipError_t launch_route(RouteArgs a, int BH, hipStream_t stream) {
   const int per = (a.nk + 63) / 64;
+  // Score GEMM on fp32 MFMA for the common head dims (score rows up to 2048
+  // columns fit the LDS row buffer); the vector-ALU kernel covers the rest.
+  if (MODE != kTopkOnly && per <= 32) {
+    if (a.D == 128) return launch_route_mfma<MODE, 128>(a, BH, stream);
+    if (a.D == 64) return launch_route_mfma<MODE, 64>(a, BH, stream);
+  }
   if (per <= 1) return launch_route_n<1, MODE>(a, BH, stream);
   if (per <= 2) return launch_route_n<2, MODE>(a, BH, stream);
   if (per <= 4) return launch_route_n<4, MODE>(a, BH, stream);
