@@ -35,7 +35,9 @@
 //   * K(j+1) is fetched while tile j's softmax and PV run, V(j+1) while
 //     tile j+1's QK^T runs (single-buffered K and V, explicit vmcnt waits);
 //     workgroups are ordered so each XCD sweeps the q-blocks of one head
-//     (shared K/V in its L2);
+//     (shared K/V in its L2), and each workgroup starts its ascending list at
+//     a block index set by its launch slot, so the workgroups resident on an
+//     XCD walk a narrow window of K/V blocks together;
 //   * the routing list is read 64 entries at a time; each lane turns its entry
 //     into the block's first token once, so a tile costs one v_readlane;
 //   * the output tile is staged through LDS and written as whole rows.
@@ -112,11 +114,10 @@ struct TileList {
     tok = ok ? block_base_token(g, n) : -1;
     valid = __ballot(ok);
   }
-  // First j' >= j whose entry is valid, or top_k.  j uniform and
-  // non-decreasing across calls.
+  // First j' >= j whose entry is valid, or top_k.  j uniform.
   __device__ int next(int j, const Geom& g) {
     while (j < top_k) {
-      if (j - base >= 64) load(j & ~63, g);
+      if (j < base || j - base >= 64) load(j & ~63, g);
       const uint64_t m = valid >> (j - base);
       if (m) return j + (int)__builtin_ctzll(m);
       j = base + 64;
@@ -125,6 +126,20 @@ struct TileList {
   }
   // First token of entry j (valid, within the current chunk).
   __device__ int32_t token(int j) const { return __builtin_amdgcn_readlane(tok, j - base); }
+  // Number of entries before the first one >= n0 in an ascending list (for
+  // any list: the count of leading entries < n0, which is a valid start).
+  __device__ int count_below(int n0, const Geom& g) {
+    int cnt = 0;
+    for (int b = 0; b < top_k; b += 64) {
+      if (b != base) load(b, g);
+      const int j = b + lane_id();
+      const int n = j < top_k ? list[j] : 0x7fffffff;
+      const int c = __popcll(__ballot(n < n0));
+      cnt += c;
+      if (c < 64) break;
+    }
+    return cnt;
+  }
 };
 
 template <int N>
@@ -298,14 +313,35 @@ void attn_mfma_kernel(AttnParams p) {
   const float sl2 = p.scale_log2;   // >= 0 on this path
 
   TileList list(p.idx + ((int64_t)bh * p.nb + qb) * p.top_k, p.top_k, p.nb, p.g);
-  int j = list.next(0, p.g);
+  // Tile order: the list rotated to start at the first entry >= n0, where
+  // n0 follows this workgroup's launch slot across [0, nb).  Workgroups that
+  // are resident together start near the same block index and then advance
+  // through their ascending lists at about the same pace, so together they
+  // sweep a narrow window of K/V blocks that stays in L2.  The softmax is
+  // order independent; the order is a function of blockIdx only.
+  constexpr int kResident = 128;  // workgroups resident per XCD (32 CUs x 4)
+  const int slot = blockIdx.x / kNumXcd;
+  const int n0 = (int)(((int64_t)(slot % kResident) * p.nb) / kResident);
+  const int j0 = list.count_below(n0, p.g);
+  // Next valid position in rotated order after position j (j < 0: start);
+  // returns top_k at the end.
+  auto next_rot = [&](int j) -> int {
+    if (j < 0 || j >= j0) {
+      const int r = list.next(j < 0 ? j0 : j + 1, p.g);
+      if (r < p.top_k) return r;
+      j = -1;
+    }
+    const int r = list.next(j + 1, p.g);
+    return r < j0 ? r : p.top_k;
+  };
+  int j = next_rot(-1);
   if (j < p.top_k) {
     const int32_t tok = list.token(j);
     dma_k(tok);
     dma_v(tok);
   }
   while (j < p.top_k) {
-    const int jn = list.next(j + 1, p.g);
+    const int jn = next_rot(j);
     const int32_t njn = jn < p.top_k ? list.token(jn) : 0;
     // In flight (oldest first): K(j), V(j).
     wait_vmcnt<C::kDmaPerWave>();
