@@ -21,11 +21,12 @@
 //     registers and every lane owns one query row: the online-softmax max/sum
 //     need one cross-lane exchange (lane ^ 32, v_permlane32_swap) and the O
 //     rescale is lane-local;
-//   * the running max is raised only when a row's tile max exceeds it by more
-//     than 2^8 (a wave-uniform branch), so the O rescale runs on few tiles;
-//     P = exp2(s*scale*log2e - m) <= 256 and its fp16/bf16 copy feeds both
-//     the PV product and the row sum (v_dot2), so numerator and denominator
-//     stay consistent;
+//   * the exponent offset m of a row is the max of its first tile; later
+//     tiles compute P = exp2(s*scale*log2e - m) without a max pass, and only
+//     when a tile's P sum exceeds 2^15 (a wave-uniform branch) is m raised to
+//     the tile max, O and l rescaled and the tile redone, so P <= 2^15 stays
+//     a normal fp16/bf16 value; its rounded copy feeds both the PV product
+//     and the row sum (v_dot2), so numerator and denominator agree;
 //   * K and V tiles go from HBM straight into LDS with buffer_load ... lds
 //     (no register staging), row-major with 16-byte chunks XOR-swizzled by
 //     row so that every operand read is bank-conflict free: K rows are read
@@ -50,8 +51,9 @@
 namespace lcv {
 namespace {
 
-// Running-max slack of the lazy online softmax, in log2 units.
-constexpr float kRescaleSlack = 8.0f;
+// MFMA kernel: a tile is redone against a raised offset when the partial sum
+// of its P values exceeds this (so every P <= 2^15, a normal fp16 value).
+constexpr float kMaxTileSum = 32768.0f;
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit dwords (gfx9 family)
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -308,8 +310,9 @@ void attn_mfma_kernel(AttnParams p) {
   for (int md = 0; md < D / 32; ++md)
 #pragma unroll
     for (int i = 0; i < 16; ++i) oacc[md][i] = 0.0f;
-  float m_run = -__builtin_inff();  // running max of s*scale*log2e (this row)
-  float l_run = 0.0f;               // this lane's partial row sum
+  float m_run = 0.0f;  // exponent offset of this row (set by the first tile)
+  float l_run = 0.0f;  // this lane's partial row sum
+  bool first = true;   // wave-uniform
   const float sl2 = p.scale_log2;   // >= 0 on this path
 
   TileList list(p.idx + ((int64_t)bh * p.nb + qb) * p.top_k, p.top_k, p.nb, p.g);
@@ -379,34 +382,50 @@ void attn_mfma_kernel(AttnParams p) {
     __syncthreads();  // both waves done reading K(j)
     if (jn < p.top_k) dma_k(njn);  // overlaps softmax + PV
 
-    // Online softmax for this lane's query row (keys split between g = 0, 1).
-    float mx = fmax3(sacc[0][0], sacc[1][0], sacc[0][1]);
-    mx = fmax3(mx, sacc[1][1], sacc[1][1]);
+    // Online softmax for this lane's query row (keys split between g = 0,
+    // 1).  The offset m_run is the row max of the first tile; later tiles
+    // are exponentiated against it directly, and only if a tile's P would
+    // exceed 2^15 (its partial sum says so; NaN included) is the offset
+    // raised to the tile max, O and l rescaled and the tile redone.  P stays
+    // a normal fp16/bf16 value, so no per-tile max is computed.
+    auto rowmax = [&]() {
+      float mx = fmax3(sacc[0][0], sacc[1][0], sacc[0][1]);
+      mx = fmax3(mx, sacc[1][1], sacc[1][1]);
 #pragma unroll
-    for (int i = 2; i < 16; ++i) mx = fmax3(mx, sacc[0][i], sacc[1][i]);
-    mx = max_halves(mx) * sl2;
-    if (__ballot(mx > m_run + kRescaleSlack)) {  // wave-uniform
-      const float m_new = fmax3(m_run, mx, mx);
-      const float corr = fast_exp2(m_run - m_new);  // 0 on the first tile
+      for (int i = 2; i < 16; ++i) mx = fmax3(mx, sacc[0][i], sacc[1][i]);
+      return max_halves(mx) * sl2;
+    };
+    // P^T as the B operand: step s takes accumulator values 8s .. 8s+7, the
+    // key runs 16s + 4g + {0..3} and 16s + 8 + 4g + {0..3}.
+    vec8 pf[4];
+    auto exps = [&]() {
+      float ls = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int flat = 8 * s + jj;
+          pf[s][jj] = from_f32<T>(fast_exp2(fmaf(sacc[flat / 16][flat % 16], sl2, -m_run)));
+        }
+        ls = Mfma<T>::sum8(pf[s], ls);
+      }
+      return ls;
+    };
+    if (first) m_run = rowmax();  // wave-uniform; O and l are still 0
+    float ls = exps();
+    if (__ballot(!(ls <= kMaxTileSum))) {  // wave-uniform, rare
+      const float m_new = fmax3(m_run, rowmax(), m_run);
+      const float corr = fast_exp2(m_run - m_new);
       l_run *= corr;
 #pragma unroll
       for (int md = 0; md < D / 32; ++md)
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[md][i] *= corr;
       m_run = m_new;
+      ls = exps();
     }
-    // P^T as the B operand: step s takes accumulator values 8s .. 8s+7, the
-    // key runs 16s + 4g + {0..3} and 16s + 8 + 4g + {0..3}.
-    vec8 pf[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const int flat = 8 * s + jj;
-        pf[s][jj] = from_f32<T>(fast_exp2(fmaf(sacc[flat / 16][flat % 16], sl2, -m_run)));
-      }
-      l_run = Mfma<T>::sum8(pf[s], l_run);
-    }
+    l_run += ls;
+    first = false;
 
     // In flight: V(j) [, K(j+1)].
     if (jn < p.top_k)

@@ -380,3 +380,25 @@ def test_attention_launch_order_changes_only_rounding(device, dtype):
     for name in ("schedule", "random"):
         d = (outs[name].float() - outs["identity"].float()).abs().max().item()
         assert d <= 4 * ulp, f"order={name}: max |diff| {d:.3g} > 4 ulp"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("q_scale", [1.0, 6.0, 12.0])
+def test_attn_wide_score_range_rescales(device, dtype, q_scale):
+    """Scores that grow along each routing list (K block j scaled by 1 + j/4)
+    and large q scales push later tiles far above the first tile's max, so
+    the exponent offset is raised (and O, l rescaled) many times per row."""
+    from lcv_bsa import bsa_attention_hip
+
+    shape, chunk = (1, 1, 2048), (1, 1, 64)
+    nb = 32
+    q = _rand((1, 2, 2048, 128), torch.float32, device, seed=31) * q_scale
+    k = _rand((1, 2, 2048, 128), torch.float32, device, seed=32)
+    k = k * (1.0 + torch.arange(2048, device=device).div(64, rounding_mode="floor").float() / 4.0)[None, None, :, None]
+    v = _rand((1, 2, 2048, 128), torch.float32, device, seed=33)
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    idx = np.broadcast_to(np.arange(0, nb, 2, dtype=np.int32), (1, 2, nb, nb // 2)).copy()
+    idx[0, 1] = idx[0, 1, :, ::-1]  # descending lists too
+    out = bsa_attention_hip(q, k, v, torch.from_numpy(idx).to(device), chunk, shape)
+    ref = O.sparse_attention_from_indices(_np(q), _np(k), _np(v), idx, shape, chunk)
+    assert_close_report(_np(out), ref, *TOL[dtype], f"wide range q*{q_scale} {dtype}")
