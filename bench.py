@@ -110,6 +110,94 @@ def cpu_baseline(w, budget_s: float):
     }
 
 
+def bench_prepare(lib, w, dev, stream, steps: int, warmup: int, seed: int):
+    """The fused pre-BSA pass (RMSNorm + 3D RoPE of q and k, block means) at the
+    workload's shape, fed the way the DiT feeds it: q / k are [B, H, S, D]
+    views of a fused QKV output [B, S, 3, H, D] (attention.py:191-201).
+
+    HBM-bound: per (q or k, batch, head, 64-token block) it reads and writes
+    64 x D elements and writes D fp32 means.  The reference's unfused chain
+    (fp32 RMSNorm -> rounded -> weight -> fp32 RoPE -> rounded, then the
+    pooling) is timed beside it in torch on the same GPU."""
+    import torch
+
+    from lcv_bsa import _lib
+    from lcv_bsa.block_sparse_attention import _geom, _strides
+    from lcv_bsa.prepare import RMS_EPS, rope_table
+    from lcv_bsa.rope_3d import rope_freqs_3d, rotate_half
+
+    B, H, S, D = w.q.shape
+    nb = w.num_blocks
+    dt = w.q.dtype
+    code = {torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}[dt]
+    gen = torch.Generator(device=dev).manual_seed(seed + 1)
+    qkv = torch.randn((B, S, 3, H, D), generator=gen, device=dev, dtype=torch.float32).to(dt)
+    q, k = qkv[:, :, 0].transpose(1, 2), qkv[:, :, 1].transpose(1, 2)
+    wq = (1.0 + 0.1 * torch.randn(D, generator=gen, device=dev)).to(dt)
+    wk = (1.0 + 0.1 * torch.randn(D, generator=gen, device=dev)).to(dt)
+    grid = _lib.Grid(*(int(x) for x in w.grid))
+    n_tab = lib.lcv_bsa_rope_table_len(D, grid)
+    table = rope_table(D, w.grid, dev)
+    q_out, k_out = torch.empty((B, H, S, D), dtype=dt, device=dev), torch.empty((B, H, S, D), dtype=dt, device=dev)
+    qb = torch.empty((B, H, nb, D), dtype=torch.float32, device=dev)
+    kb = torch.empty_like(qb)
+    geom = _geom(w.shape, w.chunk_thw)
+    sh = stream.cuda_stream
+
+    def fused():
+        _lib.check(lib.lcv_bsa_prepare_qk(
+            q.data_ptr(), k.data_ptr(), code, B, H, S, D, _strides(q), _strides(k), wq.data_ptr(),
+            wk.data_ptr(), RMS_EPS, grid, table.data_ptr(), n_tab, geom, q_out.data_ptr(),
+            k_out.data_ptr(), _strides(q_out), _strides(k_out), qb.data_ptr(), kb.data_ptr(), sh),
+            "prepare_qk")
+
+    f = rope_freqs_3d(tuple(w.grid), D, dev)
+    cos, sin = torch.cos(f), torch.sin(f)
+
+    def unfused():
+        outs = []
+        for x, wt in ((q, wq), (k, wk)):
+            xf = x.float()
+            y = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + RMS_EPS)).to(dt) * wt
+            yf = y.float()
+            r = (yf * cos + rotate_half(yf) * sin).to(dt)
+            outs.append(r.reshape(B, H, nb, 64, D).float().mean(3))
+        return outs
+
+    def timed(fn, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    for _ in range(warmup):
+        fused()
+    ms = timed(fused, steps)
+    unfused()
+    ms_torch = timed(unfused, max(2, steps // 4))
+    esz = q.element_size()
+    nbytes = 2 * B * H * nb * (2 * 64 * D * esz + D * 4)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del qkv, q_out, k_out
+    torch.cuda.empty_cache()
+    return {
+        "kernel": "prep_kernel",
+        "inputs": f"q, k as [B,H,S,D] views of a [B,S,3,H,D] {DTYPE_NAME[str(dt).split('.')[1]]} QKV buffer, "
+                  f"RoPE grid {tuple(w.grid)}",
+        "ms": round(ms, 4),
+        "algorithmic_bytes": nbytes,
+        "achieved": round(gbs, 1),
+        "peak": 8000.0,
+        "unit": "GB/s",
+        "frac": round(gbs / 8000.0, 4),
+        "unfused_torch_ms": round(ms_torch, 4),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,6 +208,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prepare", action="store_true", help="skip the pre-BSA prepare_qk timing")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (a known-size kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -272,6 +361,11 @@ def main() -> int:
         },
         "cpu_baseline": None,
     }
+    if w.grid and not args.no_prepare:
+        pre = bench_prepare(lib, w, dev, stream, args.steps, args.warmup, args.seed)
+        result["pre_bsa"] = pre
+        log(f"pre-BSA prepare_qk {pre['ms']:.3f} ms ({pre['achieved']:.0f} GB/s, "
+            f"{100 * pre['frac']:.1f}% of HBM); unfused torch chain {pre['unfused_torch_ms']:.3f} ms")
     if not args.no_cpu_baseline:
         t0 = time.time()
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_budget)

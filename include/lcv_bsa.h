@@ -201,6 +201,51 @@ int lcv_bsa_permute_block_major(const void* x, int dtype, int64_t B,
                                 lcv_bsa_geom g, int inverse, void* out,
                                 void* stream);
 
+/*
+ * Latent grid of the 3D RoPE (t-major token order): S = T * Hl * Wl.
+ */
+typedef struct lcv_bsa_grid {
+  int64_t T, Hl, Wl;
+} lcv_bsa_grid;
+
+/*
+ * Length (floats) of the RoPE table lcv_bsa_prepare_qk reads, for head dim D
+ * split into t / h / w parts of dt = D - 4*(D/6), dh = dw = 2*(D/6) dims
+ * (longcat_video/models/rope_3d.py:60-62).  Layout, each part row-major over
+ * [position][pair]:
+ *   cos_t[T][dt/2], sin_t[T][dt/2], cos_h[Hl][dh/2], sin_h[Hl][dh/2],
+ *   cos_w[Wl][dw/2], sin_w[Wl][dw/2]
+ * with angle(axis position p, pair i) = p / 10000^(2i / dim_axis)
+ * (rope_3d.py:65-93).  Returns 0 when D or the grid is not supported
+ * (D in {64, 128}, length <= 12288).
+ */
+int64_t lcv_bsa_rope_table_len(int64_t D, lcv_bsa_grid rope);
+
+/*
+ * Pre-BSA preparation of q and k in one pass (no reference counterpart as a
+ * single function; replaces the q_norm / k_norm / rope_3d steps of
+ * Attention.__call__, longcat_video/models/attention.py:195-201, plus
+ * mean_pool_blocks_3d, block_sparse_attention.py:67-104):
+ *   q_out = rope_3d(RMSNorm_FP32(q_in)), k_out likewise, where RMSNorm_FP32
+ *   (longcat_video/models/blocks.py:55-72) is x * rsqrt(mean(x^2) + eps) in
+ *   fp32, rounded to the dtype, times the weight (dtype [D]; NULL = ones),
+ *   and rope_3d (rope_3d.py:107-128) rotates in fp32 and rounds back;
+ *   qbar / kbar = fp32 block means of q_out / k_out ([B,H,nb,D], as
+ *   lcv_bsa_pool).
+ * fp16/bf16 only; D in {64, 128}; 64-token blocks (geometry g); rope is the
+ * latent grid of the RoPE positions (its product must be S); rope_table as
+ * described at lcv_bsa_rope_table_len.  All tensors 16-byte aligned rows.
+ */
+int lcv_bsa_prepare_qk(const void* q_in, const void* k_in, int dtype,
+                       int64_t B, int64_t H, int64_t S, int64_t D,
+                       lcv_bsa_strides q_in_strides, lcv_bsa_strides k_in_strides,
+                       const void* q_weight, const void* k_weight, float eps,
+                       lcv_bsa_grid rope, const float* rope_table,
+                       int64_t rope_table_len, lcv_bsa_geom g,
+                       void* q_out, void* k_out, lcv_bsa_strides q_out_strides,
+                       lcv_bsa_strides k_out_strides, float* qbar, float* kbar,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

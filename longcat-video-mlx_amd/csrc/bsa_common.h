@@ -76,6 +76,31 @@ __device__ __forceinline__ int32_t block_base_token(const Geom& g, int32_t n) {
   return bt * g.cT * g.HW + bh * g.cH * g.Wl + bw * g.cW;
 }
 
+// Division by a run-time invariant divisor with a multiply-high, exact for
+// every 32-bit unsigned numerator (Granlund & Montgomery, "Division by
+// Invariant Integers using Multiplication", PLDI 1994, figure 4.1):
+//   l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1,
+//   t = mulhi(m, n),  n / d = (t + ((n - t) >> min(l, 1))) >> max(l - 1, 0).
+struct FastDiv {
+  uint32_t d, m, s1, s2;
+};
+
+__host__ inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((uint64_t{1} << l) < d) ++l;
+  FastDiv f;
+  f.d = d;
+  f.m = (uint32_t)(((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1);
+  f.s1 = l > 0 ? 1u : 0u;
+  f.s2 = l > 0 ? l - 1 : 0u;
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv& f) {
+  const uint32_t t = __umulhi(f.m, n);
+  return (t + ((n - t) >> f.s1)) >> f.s2;
+}
+
 // Token offset of row r inside any block, relative to the block's first token.
 __device__ __forceinline__ int32_t voxel_row_offset(const Geom& g, int32_t r) {
   const int32_t plane = g.cH * g.cW;
@@ -174,6 +199,19 @@ bool attn_uses_mfma(int dtype, int D);
 hipError_t launch_schedule(const int32_t* idx, int BH, int nq, int top_k, int32_t* order,
                            hipStream_t stream);
 bool schedule_supported(int nq);
+
+// Fused RMSNorm + 3D RoPE + block means of q and k (fp16/bf16, D 64/128).
+// The RoPE table holds cos and sin per axis: [rT*dt/2 | rT*dt/2 | rH*dh/2 |
+// rH*dh/2 | rW*dw/2 | rW*dw/2] floats, at most kMaxRopeTable.
+constexpr int kMaxRopeTable = 12288;
+// Token positions are split over the RoPE grid with an fp32 reciprocal, exact
+// below 2^22 tokens.
+constexpr int64_t kPrepMaxTokens = int64_t{1} << 22;
+bool prep_supported(int dtype, int D);
+hipError_t launch_prep(const Tensor4* in, const Tensor4* out, const void* const* weight,
+                       float* const* mean, int dtype, int B, int H, int D, int nb, const Geom& g,
+                       const int32_t* rope_grid, const int32_t* rope_dims, const float* table,
+                       int table_len, float eps, hipStream_t stream);
 
 hipError_t launch_token_blocks(const Geom& g, int T, int32_t* out, hipStream_t stream);
 hipError_t launch_pair_mask(const int32_t* idx, int B, int H, int nq, int top_k,

@@ -369,4 +369,64 @@ int lcv_bsa_permute_block_major(const void* x, int dtype, int64_t B, int64_t H, 
                        "lcv_bsa_permute_block_major");
 }
 
+
+int64_t lcv_bsa_rope_table_len(int64_t D, lcv_bsa_grid rope) {
+  if (!(D == 64 || D == 128) || rope.T <= 0 || rope.Hl <= 0 || rope.Wl <= 0) return 0;
+  const int64_t dt = D - 4 * (D / 6), dh = 2 * (D / 6), dw = 2 * (D / 6);
+  const int64_t len = rope.T * dt + rope.Hl * dh + rope.Wl * dw;  // cos + sin, half dims each
+  return len <= lcv::kMaxRopeTable ? len : 0;
+}
+
+int lcv_bsa_prepare_qk(const void* q_in, const void* k_in, int dtype, int64_t B, int64_t H,
+                       int64_t S, int64_t D, lcv_bsa_strides qis, lcv_bsa_strides kis,
+                       const void* q_weight, const void* k_weight, float eps, lcv_bsa_grid rope,
+                       const float* rope_table, int64_t rope_table_len, lcv_bsa_geom g,
+                       void* q_out, void* k_out, lcv_bsa_strides qos, lcv_bsa_strides kos,
+                       float* qbar, float* kbar, void* stream) {
+  if (!q_in || !k_in || !q_out || !k_out || !qbar || !kbar || !rope_table)
+    return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
+  if (!dtype_ok(dtype)) return fail(LCV_BSA_ERR_DTYPE, "unknown dtype %d", dtype);
+  if (!lcv::prep_supported(dtype, (int)D))
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "prepare_qk supports fp16/bf16 with D in {64, 128}");
+  int64_t nb = 0, bs = 0;
+  int st = check_geom(B, H, S, D, g, &nb, &bs);
+  if (st) return st;
+  if (bs != 64)
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "prepare_qk requires 64-token blocks (got %lld)",
+                (long long)bs);
+  if (rope.T <= 0 || rope.Hl <= 0 || rope.Wl <= 0 || rope.T * rope.Hl * rope.Wl != S)
+    return fail(LCV_BSA_ERR_SHAPE, "RoPE grid (%lld, %lld, %lld) must be positive with product S=%lld",
+                (long long)rope.T, (long long)rope.Hl, (long long)rope.Wl, (long long)S);
+  if (S > lcv::kPrepMaxTokens)
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "prepare_qk supports at most %lld tokens (S=%lld)",
+                (long long)lcv::kPrepMaxTokens, (long long)S);
+  const int64_t need = lcv_bsa_rope_table_len(D, rope);
+  if (need == 0)
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "RoPE table for this grid exceeds %d floats",
+                lcv::kMaxRopeTable);
+  if (rope_table_len != need)
+    return fail(LCV_BSA_ERR_INVALID_ARG, "rope_table_len=%lld, expected %lld",
+                (long long)rope_table_len, (long long)need);
+  if (!std::isfinite(eps) || eps < 0.0f) return fail(LCV_BSA_ERR_INVALID_ARG, "eps must be >= 0");
+  if ((st = check_strides("q_in", qis, D)) || (st = check_strides("k_in", kis, D)) ||
+      (st = check_strides("q_out", qos, D)) || (st = check_strides("k_out", kos, D)))
+    return st;
+  if (!vec_aligned(q_in, qis, 8) || !vec_aligned(k_in, kis, 8) || !vec_aligned(q_out, qos, 8) ||
+      !vec_aligned(k_out, kos, 8))
+    return fail(LCV_BSA_ERR_LAYOUT, "q/k rows must start on 16-byte boundaries");
+  if ((uintptr_t)q_weight % 16 || (uintptr_t)k_weight % 16 || (uintptr_t)qbar % 16 ||
+      (uintptr_t)kbar % 16)
+    return fail(LCV_BSA_ERR_LAYOUT, "norm weights and block means must be 16-byte aligned");
+  const lcv::Tensor4 in[2] = {{q_in, qis.b, qis.h, qis.s}, {k_in, kis.b, kis.h, kis.s}};
+  const lcv::Tensor4 out[2] = {{q_out, qos.b, qos.h, qos.s}, {k_out, kos.b, kos.h, kos.s}};
+  const void* w[2] = {q_weight, k_weight};
+  float* means[2] = {qbar, kbar};
+  const int32_t grid[3] = {(int32_t)rope.T, (int32_t)rope.Hl, (int32_t)rope.Wl};
+  const int32_t dims[2] = {(int32_t)(D - 4 * (D / 6)), (int32_t)(2 * (D / 6))};
+  return launch_status(lcv::launch_prep(in, out, w, means, dtype, (int)B, (int)H, (int)D, (int)nb,
+                                        lcv::make_geom(g), grid, dims, rope_table, (int)need, eps,
+                                        (hipStream_t)stream),
+                       "lcv_bsa_prepare_qk");
+}
+
 }  // extern "C"

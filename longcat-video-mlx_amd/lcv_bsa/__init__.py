@@ -24,6 +24,7 @@ from .block_sparse_attention_hip import (  # noqa: F401
     reshape_from_block_major,
     reshape_to_block_major,
 )
+from .prepare import prepare_qk, rope_table  # noqa: F401
 from .attention import BSAAttention, backend_from_env  # noqa: F401
 from .dit import BSAModelMixin, apply_bsa_params, disable_bsa, enable_bsa  # noqa: F401
 

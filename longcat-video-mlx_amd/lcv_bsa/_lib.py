@@ -38,6 +38,12 @@ class Geom(ctypes.Structure):
     _fields_ = [(n, c_int64) for n in ("T", "Hl", "Wl", "cT", "cH", "cW")]
 
 
+class Grid(ctypes.Structure):
+    """lcv_bsa_grid: latent grid (T, Hl, Wl) of the RoPE positions."""
+
+    _fields_ = [(n, c_int64) for n in ("T", "Hl", "Wl")]
+
+
 _SIGNATURES = {
     "lcv_bsa_version": (c_char_p, []),
     "lcv_bsa_strerror": (c_char_p, [c_int]),
@@ -64,6 +70,11 @@ _SIGNATURES = {
                                         c_int64, c_int64, c_void_p, c_void_p]),
     "lcv_bsa_permute_block_major": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64,
                                             Geom, c_int, c_void_p, c_void_p]),
+    "lcv_bsa_rope_table_len": (c_int64, [c_int64, Grid]),
+    "lcv_bsa_prepare_qk": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64, c_int64,
+                                   Strides, Strides, c_void_p, c_void_p, c_float, Grid, c_void_p,
+                                   c_int64, Geom, c_void_p, c_void_p, Strides, Strides, c_void_p,
+                                   c_void_p, c_void_p]),
 }
 
 EXPORTED = tuple(_SIGNATURES)
@@ -117,6 +128,6 @@ def check(status: int, what: str) -> None:
 
 
 __all__ = [
-    "BF16", "F16", "F32", "Geom", "Strides", "EXPORTED", "BSALibraryError", "LIB_PATH",
+    "BF16", "F16", "F32", "Geom", "Grid", "Strides", "EXPORTED", "BSALibraryError", "LIB_PATH",
     "check", "load", "version",
 ]

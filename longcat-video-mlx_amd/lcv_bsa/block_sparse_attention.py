@@ -267,6 +267,7 @@ def bsa_attention(
     *,
     top_k: Optional[int] = None,
     return_indices: bool = False,
+    block_means: Optional[tuple[torch.Tensor, torch.Tensor]] = None,
 ):
     """Block Sparse Attention forward (block_sparse_attention.py:201-250).
 
@@ -274,6 +275,8 @@ def bsa_attention(
     ``shape = (T, H, W)`` must be a multiple of ``chunk_thw`` whose product
     is 64.  Returns ``[B, H, S, D]`` in q's dtype, or ``(out, indices)`` with
     ``return_indices=True`` (indices ``[B, H, nb, top_k]`` int32, ascending).
+    ``block_means=(q_blocks, k_blocks)`` (fp32 ``[B, H, nb, D]``, e.g. from
+    ``prepare_qk``) skips the pooling pass.
     """
     _require_device(q, k, v)
     q, k, v = _bhsd(q, "q"), _bhsd(k, "k"), _bhsd(v, "v")
@@ -289,6 +292,16 @@ def bsa_attention(
     kk = num_selected_blocks(nb, sparsity) if top_k is None else int(top_k)
     if not 1 <= kk <= nb:
         raise ValueError(f"top_k={kk} must be in [1, {nb}]")
+    if block_means is not None:
+        qb, kb = block_means
+        for name, t in (("q_blocks", qb), ("k_blocks", kb)):
+            if tuple(t.shape) != (B, H, nb, D) or t.dtype != torch.float32:
+                raise ValueError(f"{name} must be fp32 [{B}, {H}, {nb}, {D}], got {tuple(t.shape)} {t.dtype}")
+        from .block_sparse_attention_hip import bsa_attention_hip
+
+        idx = select_block_indices(qb, kb, kk)
+        out = bsa_attention_hip(q, k, v, idx, chunk_thw, shape, sm_scale)
+        return (out, idx) if return_indices else out
     code = _dtype_code(q)
     if code != _lib.F32:
         q, k, v = _aligned_rows(q), _aligned_rows(k), _aligned_rows(v)

@@ -26,7 +26,7 @@ __all__ = [
     "build_token_block_indices", "build_token_pair_mask", "sdpa", "bsa_attention",
     "bsa_attention_masked", "sparse_attention_from_indices", "reshape_to_block_major",
     "reshape_from_block_major", "block_tokens", "rope_dims", "rope_freqs_3d", "rotate_half",
-    "apply_rope", "executed_flops",
+    "apply_rope", "executed_flops", "round_to", "rms_norm_fp32", "prepare_qk",
 ]
 
 
@@ -269,6 +269,49 @@ def apply_rope(x, freqs):
     xf = np.asarray(x).astype(np.float32)
     c, s = np.cos(freqs).astype(np.float32), np.sin(freqs).astype(np.float32)
     return xf * c + rotate_half(xf) * s
+
+
+# --- blocks.py:55-72 (RMSNorm_FP32), attention.py:191-201 -------------------
+def round_to(x, dtype: str):
+    """Round fp32 values to fp16 / bf16 (nearest even) and widen back to fp32."""
+    x = np.asarray(x, dtype=np.float32)
+    if dtype == "f16":
+        return x.astype(np.float16).astype(np.float32)
+    if dtype == "bf16":
+        u = x.view(np.uint32).astype(np.uint64)
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+        out = r.astype(np.uint32).view(np.float32)
+        return np.where(np.isnan(x), x, out)
+    return x
+
+
+def rms_norm_fp32(x, weight=None, eps=1e-6, dtype="f16"):
+    """RMSNorm_FP32 (blocks.py:55-72): x * rsqrt(mean(x^2) + eps) in fp32,
+    rounded to the input dtype, then times the weight in that dtype."""
+    x = np.asarray(x, dtype=np.float32)
+    ms = np.mean(x * x, axis=-1, keepdims=True, dtype=np.float32)
+    y = round_to(x * (np.float32(1.0) / np.sqrt(ms + np.float32(eps))), dtype)
+    if weight is None:
+        return y
+    return round_to(y * round_to(np.asarray(weight, dtype=np.float32), dtype), dtype)
+
+
+def prepare_qk(q, k, grid, shape=None, chunk_thw=(4, 4, 4), q_weight=None, k_weight=None,
+               eps=1e-6, dtype="f16"):
+    """q_norm / k_norm then rope_3d (attention.py:195-201; RoPE in fp32 and
+    rounded back, rope_3d.py:120-128), then the block means of the results
+    (block_sparse_attention.py:67-104).  Returns q, k (dtype values as fp32)
+    and their fp64 block means."""
+    shape = tuple(grid) if shape is None else tuple(shape)
+    f = rope_freqs_3d(grid, np.asarray(q).shape[-1]).astype(np.float32)
+    cos, sin = np.cos(f), np.sin(f)
+    outs = []
+    for x, w in ((q, q_weight), (k, k_weight)):
+        y = rms_norm_fp32(x, w, eps, dtype)
+        r = round_to(y * cos + rotate_half(y) * sin, dtype)
+        outs.append(r)
+    means = [mean_pool_blocks_3d(o, shape, chunk_thw) for o in outs]
+    return outs[0], outs[1], means[0], means[1]
 
 
 def executed_flops(B, H, nq, k, D, bs=64):

@@ -22,7 +22,7 @@ NO_GPU = not torch.cuda.is_available()
 
 def _declared():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:const char\*|int|size_t)\s+(lcv_bsa_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int|int64_t|size_t)\s+(lcv_bsa_\w+)\s*\(", text, re.M)))
 
 
 def test_header_and_binding_agree():
@@ -101,6 +101,38 @@ def test_c_abi_validation_returns_before_launch():
     with pytest.raises(ValueError, match="multiple of"):
         _lib.check(lib.lcv_bsa_pool(fake, 0, 1, 1, 96, 8, S_(768, 768, 8), G(4, 4, 6, 4, 4, 4),
                                     fake, None), "pool")
+
+
+def test_prepare_qk_validation_and_table_length():
+    """lcv_bsa_prepare_qk argument checks (no launch) and the table size."""
+    from lcv_bsa import _lib, rope_table
+
+    lib = _lib.load()
+    S_, G, R = _lib.Strides, _lib.Geom, _lib.Grid
+    n = lib.lcv_bsa_rope_table_len(128, R(16, 45, 80))
+    assert n == 2 * (16 * 22 + 45 * 21 + 80 * 21)
+    assert rope_table(128, (16, 45, 80)).numel() == n  # CPU tensor: same layout size
+    assert lib.lcv_bsa_rope_table_len(64, R(2, 3, 4)) == 2 * (2 * 12 + 3 * 10 + 4 * 10)
+    assert lib.lcv_bsa_rope_table_len(96, R(2, 3, 4)) == 0  # D unsupported
+    assert lib.lcv_bsa_rope_table_len(128, R(64, 200, 300)) == 0  # table too large
+    fake = 4096
+    st_ = S_(4096 * 128, 4096 * 128, 128)
+    g = G(1, 1, 4096, 1, 1, 64)
+
+    def call(dtype=0, D=128, rope=R(4, 16, 64), tlen=None, geom=g, q=fake, eps=1e-6, strides=st_):
+        tl = lib.lcv_bsa_rope_table_len(D, rope) if tlen is None else tlen
+        return lib.lcv_bsa_prepare_qk(q, fake, dtype, 1, 1, 4096, D, strides, strides, None, None, eps,
+                                      rope, fake, tl, geom, fake, fake, strides, strides, fake, fake, None)
+
+    assert call(dtype=2) == _lib.ERR_UNSUPPORTED  # fp32
+    assert call(dtype=9) == _lib.ERR_DTYPE
+    assert call(D=96, strides=S_(4096 * 96, 4096 * 96, 96)) == _lib.ERR_UNSUPPORTED
+    assert call(rope=R(4, 16, 32)) == _lib.ERR_SHAPE and b"RoPE grid" in lib.lcv_bsa_last_error()
+    assert call(tlen=7) == _lib.ERR_INVALID_ARG and b"rope_table_len" in lib.lcv_bsa_last_error()
+    assert call(geom=G(1, 2, 2048, 1, 2, 16)) == _lib.ERR_UNSUPPORTED  # 32-token blocks
+    assert call(q=fake + 2) == _lib.ERR_LAYOUT
+    assert call(eps=-1.0) == _lib.ERR_INVALID_ARG
+    assert call(q=None) == _lib.ERR_INVALID_ARG
 
 
 def test_python_api_rejects_cpu_tensors_loudly():

@@ -331,3 +331,66 @@ def test_planted_missing_voxel_transpose_is_caught():
 def test_planted_floor_vs_ceil_is_caught():
     ceil_rule = lambda nk, sp: max(1, math.ceil((1.0 - sp) * nk))
     assert ceil_rule(900, 0.9375) != O.num_selected(900, 0.9375)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm_FP32 and dtype rounding (blocks.py:55-72; attention.py:195-201)
+# ---------------------------------------------------------------------------
+
+def test_round_to_matches_torch_and_ties_to_even():
+    x = RNG.normal(size=4096).astype(np.float32) * np.float32(100.0)
+    for name, dt in (("f16", torch.float16), ("bf16", torch.bfloat16)):
+        ref = torch.from_numpy(x).to(dt).float().numpy()
+        assert np.array_equal(O.round_to(x, name), ref), name
+    one = np.float32(1.0)
+    assert O.round_to(one + np.float32(2.0 ** -11), "f16") == 1.0           # tie -> even
+    assert O.round_to(one + np.float32(3 * 2.0 ** -11), "f16") == one + np.float32(2.0 ** -9)
+    assert O.round_to(one + np.float32(2.0 ** -8), "bf16") == 1.0           # tie -> even
+    assert O.round_to(one + np.float32(3 * 2.0 ** -8), "bf16") == one + np.float32(2.0 ** -6)
+    assert np.isnan(O.round_to(np.float32(np.nan), "bf16"))
+    assert O.round_to(np.float32(np.inf), "bf16") == np.inf
+
+
+def test_rms_norm_known_answers():
+    # [3, 4]: mean(x^2) = 12.5, so x / sqrt(12.5) (eps 0 here).
+    got = O.rms_norm_fp32(np.array([[3.0, 4.0]]), eps=0.0, dtype="f32")
+    assert np.allclose(got, np.array([[3.0, 4.0]]) / math.sqrt(12.5), rtol=1e-6)
+    # a constant row normalises to +-1 (up to eps); the weight scales per column.
+    c = np.full((2, 8), -7.0, np.float32)
+    assert np.allclose(O.rms_norm_fp32(c, eps=1e-6, dtype="f32"), -1.0, atol=1e-6)
+    w = np.arange(1, 9, dtype=np.float32)
+    assert np.allclose(O.rms_norm_fp32(c, w, eps=1e-6, dtype="f32"), -w, rtol=1e-6)
+    # fp16 / bf16: fp64 truth rounded to the dtype (normalisation) and again
+    # after the weight; one dtype ulp at most from the double-precision value.
+    x = RNG.normal(size=(64, 128)).astype(np.float32)
+    wt = (1.0 + 0.1 * RNG.normal(size=128)).astype(np.float32)
+    for name, ulp in (("f16", 2.0 ** -10), ("bf16", 2.0 ** -7)):
+        wq = O.round_to(wt, name)
+        x64 = x.astype(np.float64)
+        truth = x64 / np.sqrt(np.mean(x64 * x64, axis=-1, keepdims=True) + 1e-6) * wq
+        got = O.rms_norm_fp32(x, wt, 1e-6, name)
+        assert np.all(np.abs(got - truth) <= 2 * ulp * np.maximum(np.abs(truth), 1.0)), name
+
+
+def test_planted_rms_sum_instead_of_mean_is_caught():
+    x = RNG.normal(size=(4, 128)).astype(np.float32)
+    planted = x / np.sqrt(np.sum(x * x, axis=-1, keepdims=True) + 1e-6)
+    assert not np.allclose(planted, O.rms_norm_fp32(x, eps=1e-6, dtype="f32"), rtol=1e-3)
+
+
+def test_prepare_qk_composes_the_pinned_steps():
+    """prepare_qk == rms_norm -> RoPE (fp32, rounded) -> block means; with a
+    one-position grid RoPE is the identity."""
+    q = RNG.normal(size=(1, 2, 64, 64)).astype(np.float32)
+    k = RNG.normal(size=(1, 2, 64, 64)).astype(np.float32)
+    qo, ko, qb, kb = O.prepare_qk(q, k, (1, 1, 64), chunk_thw=(1, 1, 64), dtype="f16")
+    r = O.rms_norm_fp32(q, None, 1e-6, "f16")
+    f = O.rope_freqs_3d((1, 1, 64), 64).astype(np.float32)
+    assert np.array_equal(qo, O.round_to(r * np.cos(f) + O.rotate_half(r) * np.sin(f), "f16"))
+    assert np.allclose(qb, O.mean_pool_blocks_3d(qo, (1, 1, 64), (1, 1, 64)))
+    # Position 0 on every axis: cos = 1, sin = 0.
+    q1 = RNG.normal(size=(1, 1, 64, 64)).astype(np.float32)
+    qo1, _, _, _ = O.prepare_qk(q1, q1, (64, 1, 1), shape=(1, 1, 64), chunk_thw=(1, 1, 64))
+    f1 = O.rope_freqs_3d((64, 1, 1), 64)
+    assert np.all(f1[0] == 0.0)
+    assert np.array_equal(qo1[..., 0, :], O.rms_norm_fp32(q1, None, 1e-6, "f16")[..., 0, :])
