@@ -198,6 +198,105 @@ def bench_prepare(lib, w, dev, stream, steps: int, warmup: int, seed: int):
     }
 
 
+def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int):
+    """One LongCat DiT block at 720p (longcat_video_dit.py:36-138): hidden
+    4096, 32 heads of 128, SwiGLU inner 11008, AdaLN from a 512-wide timestep
+    embedding per frame, 512 text tokens, latent grid 16 x 45 x 80, bf16,
+    random weights.  The self-attention runs the fused pre-BSA pass and BSA
+    (64-token blocks, top-k ``top_k``); the linear layers are torch GEMMs.
+
+    A first timed region runs whole blocks; a second attributes time to the
+    sub-modules with events recorded by forward hooks.  The BSA share is the
+    self-attention minus its two GEMMs: prepare_qk + routing + attention."""
+    import torch
+
+    from lcv_bsa.dit_block import LongCatSingleStreamBlock
+
+    grid, C, H, L, t_dim = (16, 45, 80), 4096, 32, 512, 512
+    N = grid[0] * grid[1] * grid[2]
+    torch.manual_seed(seed + 2)
+    blk = LongCatSingleStreamBlock(C, H, 4, t_dim, dtype=torch.bfloat16, device=dev)
+    with torch.no_grad():
+        for name, p in blk.named_parameters():
+            if name.endswith("norm.weight") or name == "pre_crs_attn_norm.weight":
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, 0.02)
+    blk.attn.enable_bsa, blk.attn.bsa_shape_policy, blk.attn.bsa_top_k = True, "auto", top_k
+    gen = torch.Generator(device=dev).manual_seed(seed + 3)
+    x = torch.randn((1, N, C), generator=gen, device=dev).to(torch.bfloat16)
+    y = torch.randn((1, L, C), generator=gen, device=dev).to(torch.bfloat16)
+    t = torch.randn((1, grid[0], t_dim), generator=gen, device=dev)
+
+    def step():
+        with torch.no_grad():
+            return blk(x, y, t, [L], grid)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    assert blk.attn.last_path == "bsa"
+
+    marks: dict = {}
+    mods = {"self_attn": blk.attn, "qkv_gemm": blk.attn.qkv, "proj_gemm": blk.attn.proj,
+            "cross_attn": blk.cross_attn, "pre_cross_norm": blk.pre_crs_attn_norm, "ffn": blk.ffn}
+    handles = []
+    for name, m in mods.items():
+        def pre(mod, inp, name=name):
+            e = torch.cuda.Event(enable_timing=True)
+            e.record(stream)
+            marks.setdefault(name, []).append([e, None])
+
+        def post(mod, inp, out, name=name):
+            e = torch.cuda.Event(enable_timing=True)
+            e.record(stream)
+            marks[name][-1][1] = e
+        handles += [m.register_forward_pre_hook(pre), m.register_forward_hook(post)]
+    b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    b0.record(stream)
+    for _ in range(steps):
+        step()
+    b1.record(stream)
+    torch.cuda.synchronize()
+    for h in handles:
+        h.remove()
+    per = {k: sum(a.elapsed_time(b) for a, b in v) / steps for k, v in marks.items()}
+    ms_instr = b0.elapsed_time(b1) / steps
+    bsa_ms = per["self_attn"] - per["qkv_gemm"] - per["proj_gemm"]
+    Hf = blk.ffn.hidden_dim
+    gemm_flop = 2 * N * C * (3 * C + C + C + C + 3 * Hf) + 2 * L * C * 2 * C
+    ffn_ms = per["ffn"]
+    other = ms_instr - per["self_attn"] - per["cross_attn"] - per["pre_cross_norm"] - ffn_ms
+    del blk, x, y, t
+    torch.cuda.empty_cache()
+    return {
+        "workload": "one LongCat-Video DiT block, 720p refinement latents (16, 45, 80) = 57600 tokens, hidden 4096, "
+                    "32 heads x 128, SwiGLU 11008, 512 text tokens, bf16, random weights",
+        "dtype": "bf16",
+        "bsa": f"fused prepare_qk + BSA, 64-token blocks, top-k {top_k} of 900",
+        "ms": round(ms, 3),
+        "bsa_ms": round(bsa_ms, 3),
+        "bsa_share": round(bsa_ms / ms_instr, 4),
+        "breakdown_ms": {
+            "self_attn_qkv_gemm": round(per["qkv_gemm"], 3),
+            "self_attn_bsa (prepare_qk + routing + attention)": round(bsa_ms, 3),
+            "self_attn_proj_gemm": round(per["proj_gemm"], 3),
+            "cross_attn (norm, 3 GEMMs, SDPA over 512 text tokens)": round(per["cross_attn"] + per["pre_cross_norm"], 3),
+            "ffn (3 GEMMs + SiLU gate)": round(ffn_ms, 3),
+            "adaln_modulation_and_residuals": round(other, 3),
+        },
+        "gemm_tflop": round(gemm_flop / 1e12, 3),
+        "instrumented_ms": round(ms_instr, 3),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -209,6 +308,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prepare", action="store_true", help="skip the pre-BSA prepare_qk timing")
+    ap.add_argument("--no-dit-block", action="store_true", help="skip the 720p DiT block timing")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (a known-size kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -366,6 +466,11 @@ def main() -> int:
         result["pre_bsa"] = pre
         log(f"pre-BSA prepare_qk {pre['ms']:.3f} ms ({pre['achieved']:.0f} GB/s, "
             f"{100 * pre['frac']:.1f}% of HBM); unfused torch chain {pre['unfused_torch_ms']:.3f} ms")
+    if args.config == "c2" and not args.no_dit_block:
+        blk = bench_dit_block(dev, stream, max(3, args.steps // 2), 2, args.seed, top_k)
+        result["dit_block"] = blk
+        log(f"DiT block 720p bf16: {blk['ms']:.2f} ms, BSA {blk['bsa_ms']:.2f} ms = "
+            f"{100 * blk['bsa_share']:.1f} % ({blk['breakdown_ms']})")
     if not args.no_cpu_baseline:
         t0 = time.time()
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_budget)

@@ -50,8 +50,29 @@ def backend_from_env(default: str = DEFAULT_BACKEND) -> str:
 
 
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float) -> torch.Tensor:
-    """Dense SDPA, the dispatcher's fallback (attention.py:179)."""
-    return F.scaled_dot_product_attention(q, k, v, scale=scale)
+    """Dense SDPA, the dispatcher's fallback (attention.py:179).
+
+    On the GPU only torch's fused SDPA kernels are used, never its math path
+    (its batched products take a transposed bf16 operand); where no fused
+    kernel applies, the scores are formed in fp32 over row chunks with
+    contiguous operands.  On the CPU, plain SDPA."""
+    if q.device.type != "cuda":
+        return F.scaled_dot_product_attention(q, k, v, scale=scale)
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(q, k, v, scale=scale)
+    except RuntimeError:
+        pass
+    kt = k.float().transpose(-1, -2).contiguous()
+    vf = v.float().contiguous()
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    step = 4096
+    for s0 in range(0, q.shape[-2], step):
+        s = torch.matmul(q[..., s0:s0 + step, :].float().contiguous(), kt) * scale
+        out[..., s0:s0 + step, :] = torch.matmul(torch.softmax(s, dim=-1), vf).to(q.dtype)
+    return out
 
 
 class BSAAttention:

@@ -268,6 +268,7 @@ def bsa_attention(
     top_k: Optional[int] = None,
     return_indices: bool = False,
     block_means: Optional[tuple[torch.Tensor, torch.Tensor]] = None,
+    out: Optional[torch.Tensor] = None,
 ):
     """Block Sparse Attention forward (block_sparse_attention.py:201-250).
 
@@ -276,7 +277,9 @@ def bsa_attention(
     is 64.  Returns ``[B, H, S, D]`` in q's dtype, or ``(out, indices)`` with
     ``return_indices=True`` (indices ``[B, H, nb, top_k]`` int32, ascending).
     ``block_means=(q_blocks, k_blocks)`` (fp32 ``[B, H, nb, D]``, e.g. from
-    ``prepare_qk``) skips the pooling pass.
+    ``prepare_qk``) skips the pooling pass.  ``out`` is an optional
+    ``[B, H, S, D]`` destination with unit last stride (e.g. a head-major
+    view of a ``[B, S, H, D]`` buffer).
     """
     _require_device(q, k, v)
     q, k, v = _bhsd(q, "q"), _bhsd(k, "k"), _bhsd(v, "v")
@@ -300,13 +303,15 @@ def bsa_attention(
         from .block_sparse_attention_hip import bsa_attention_hip
 
         idx = select_block_indices(qb, kb, kk)
-        out = bsa_attention_hip(q, k, v, idx, chunk_thw, shape, sm_scale)
+        out = bsa_attention_hip(q, k, v, idx, chunk_thw, shape, sm_scale, out=out)
         return (out, idx) if return_indices else out
     code = _dtype_code(q)
     if code != _lib.F32:
         q, k, v = _aligned_rows(q), _aligned_rows(k), _aligned_rows(v)
     lib = _lib.load()
-    out = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
+    from .block_sparse_attention_hip import _output
+
+    out = _output(out, q)
     idx = torch.empty((B, H, nb, kk), dtype=torch.int32, device=q.device)
     ws_bytes = lib.lcv_bsa_forward_workspace_bytes(B, H, nb, D)
     ws = torch.empty((ws_bytes + 255,), dtype=torch.uint8, device=q.device)

@@ -56,6 +56,8 @@ def bsa_attention_hip(
     chunk_thw: tuple[int, int, int] = (4, 4, 4),
     shape: Optional[tuple[int, int, int]] = None,
     sm_scale: Optional[float] = None,
+    *,
+    out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attend each q-block to the KV blocks listed in ``block_indices``.
 
@@ -67,7 +69,11 @@ def bsa_attention_hip(
         shape: ``(T, H, W)``; required, as in the reference.
         sm_scale: softmax scale, default ``1/sqrt(D)`` (the reference
             kernels hard-code that value, metal.py:114, 410, 636, 873).
-    Returns: ``[B, H, S, D]`` in q's dtype.
+        out: optional ``[B, H, S, D]`` destination in q's dtype with unit
+            last stride and 16-byte aligned rows, e.g. the ``transpose(1, 2)``
+            view of a ``[B, S, H, D]`` buffer, so the head merge after
+            attention needs no copy.
+    Returns: ``[B, H, S, D]`` in q's dtype (``out`` when given).
     """
     if shape is None:
         raise ValueError(
@@ -104,7 +110,7 @@ def bsa_attention_hip(
     if code != _lib.F32:
         q, k, v = _aligned_rows(q), _aligned_rows(k), _aligned_rows(v)
     order = schedule_block_order(bi) if nb <= MAX_SCHEDULED_BLOCKS else None
-    out = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
+    out = _output(out, q)
     st = _lib.load().lcv_bsa_attn_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), code, B, H, S, D,
         _strides(q), _strides(k), _strides(v), bi.data_ptr(),
@@ -112,6 +118,18 @@ def bsa_attention_hip(
         _geom(shape, chunk_thw), out.data_ptr(), _strides(out), _stream(q),
     )
     _lib.check(st, "bsa_attention_hip")
+    return out
+
+
+def _output(out: Optional[torch.Tensor], q: torch.Tensor) -> torch.Tensor:
+    """A fresh ``[B, H, S, D]`` output, or the caller's after checking it."""
+    if out is None:
+        return torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype or out.device != q.device:
+        raise ValueError(f"out must be {tuple(q.shape)} {q.dtype} on {q.device}, got "
+                         f"{tuple(out.shape)} {out.dtype} on {out.device}")
+    if out.stride(-1) != 1:
+        raise ValueError("out must have unit stride in its last dimension")
     return out
 
 

@@ -362,3 +362,52 @@ def test_golden_voxel_reproduced():
                                       return_indices=True)
     assert np.array_equal(idx, fx["indices"])
     assert np.abs(out - fx["out"]).max() < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# Shape policy and the DiT block's host side
+# ---------------------------------------------------------------------------
+
+def test_shape_policy_decisions():
+    from lcv_bsa.shape_policy import bsa_geometry
+
+    g720 = (16, 45, 80)
+    # The reference keeps (shape, chunk): BSA then raises ValueError -> dense.
+    assert bsa_geometry(g720, (4, 4, 4), "reference") == (g720, (4, 4, 4))
+    with pytest.raises(ValueError):
+        O.mean_pool_blocks_3d(np.zeros((1, 1, 57600, 8)), g720, (4, 4, 4))
+    # auto: the voxel where it tiles, else 64-token runs, else dense.
+    assert bsa_geometry((16, 48, 80), (4, 4, 4), "auto") == ((16, 48, 80), (4, 4, 4))
+    assert bsa_geometry(g720, (4, 4, 4), "auto") == ((1, 1, 57600), (1, 1, 64))
+    assert bsa_geometry((1, 3, 7), (4, 4, 4), "auto") is None
+    assert bsa_geometry((16, 48, 80), (4, 4, 4), "contiguous") == ((1, 1, 61440), (1, 1, 64))
+    with pytest.raises(ValueError):
+        bsa_geometry(g720, (4, 4, 4), "pad")
+
+
+def test_dit_block_parameters_match_checkpoint_layout():
+    """Module and parameter names / shapes of the torch block are the
+    reference's (PyTorch checkpoint keys, longcat_video_dit.py:36-66), with
+    the SwiGLU width 11008 at dim 4096."""
+    from oracle.dit_block_oracle import block_param_shapes
+
+    from lcv_bsa.dit_block import LongCatSingleStreamBlock
+
+    with torch.device("meta"):
+        blk = LongCatSingleStreamBlock(4096, 32, 4, 512)
+    sd = {k: tuple(v.shape) for k, v in blk.state_dict().items()}
+    assert sd == block_param_shapes(4096, 32, 4, 512)
+    assert blk.ffn.hidden_dim == 11008
+    assert blk.attn.bsa_shape_policy == "reference" and not blk.attn.enable_bsa
+
+
+def test_dit_block_reference_modulation_asserts_fp32():
+    from lcv_bsa.dit_block import LayerNorm_FP32, modulate_fp32
+
+    norm = LayerNorm_FP32(8, 1e-6, elementwise_affine=False)
+    x = torch.randn(1, 2, 3, 8)
+    zero = torch.zeros(1, 2, 1, 8)
+    y = modulate_fp32(norm, x, zero, zero)
+    assert torch.allclose(y, torch.nn.functional.layer_norm(x, (8,), eps=1e-6), atol=1e-6)
+    with pytest.raises(AssertionError):
+        modulate_fp32(norm, x, zero.to(torch.bfloat16), zero)
