@@ -145,6 +145,26 @@ int lcv_bsa_attn_fwd(const void* q, const void* k, const void* v, int dtype,
                      void* stream);
 
 /*
+ * lcv_bsa_attn_fwd with q and k / v of different lengths and block
+ * geometries: q and out have Sq rows cut by gq into nq 64-token blocks, k
+ * and v have Sk rows cut by gk into nk blocks; idx is a dense
+ * [B,H,nq,top_k] int32 of k/v block ids (entries outside [0, nk) are
+ * skipped) and order a per-head permutation of the nq q-blocks (nullable).
+ * This is BSA for the conditioning / KV-cache paths of the reference, where
+ * noise queries attend to cached + new keys
+ * (longcat_video/models/attention.py:218-221 and 235-275), which the
+ * reference always sends to dense attention (attention.py:89 requires
+ * S_q == S_k).  With Sq == Sk and gq == gk it is lcv_bsa_attn_fwd.
+ */
+int lcv_bsa_attn_fwd_kv(const void* q, const void* k, const void* v, int dtype,
+                        int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                        lcv_bsa_strides qs, lcv_bsa_strides ks,
+                        lcv_bsa_strides vs, const int32_t* idx,
+                        const int32_t* order, int64_t top_k, float sm_scale,
+                        lcv_bsa_geom gq, lcv_bsa_geom gk, void* out,
+                        lcv_bsa_strides os, void* stream);
+
+/*
  * Bytes of workspace lcv_bsa_forward needs: the fp32 pooled means of q and
  * k (2*B*H*nb*D*4 bytes) and the int32 launch order (B*H*nb*4 bytes), each
  * rounded up to 256 bytes.  Host only.

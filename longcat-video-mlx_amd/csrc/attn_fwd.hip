@@ -273,7 +273,7 @@ void attn_mfma_kernel(AttnParams p) {
     const int t = wave * C::kDmaPerWave + u;
     const int row = t * C::kRowsPerDma + lane / C::DC;
     const int pos = lane % C::DC;
-    const uint32_t tokoff = (uint32_t)voxel_row_offset(p.g, row);
+    const uint32_t tokoff = (uint32_t)voxel_row_offset(p.gk, row);
     kvo[u] = (tokoff * (uint32_t)p.k_ss + 8u * (pos ^ C::kswz(row))) * sizeof(T);
     vvo[u] = (tokoff * (uint32_t)p.v_ss + 8u * (pos ^ C::vswz(row))) * sizeof(T);
   }
@@ -315,26 +315,26 @@ void attn_mfma_kernel(AttnParams p) {
   bool first = true;   // wave-uniform
   const float sl2 = p.scale_log2;   // >= 0 on this path
 
-  TileList list(p.idx + ((int64_t)bh * p.nb + qb) * p.top_k, p.top_k, p.nb, p.g);
+  TileList list(p.idx + ((int64_t)bh * p.nb + qb) * p.top_k, p.top_k, p.nk, p.gk);
   // Tile order: the list rotated to start at the first entry >= n0, where
-  // n0 follows this workgroup's launch slot across [0, nb).  Workgroups that
+  // n0 follows this workgroup's launch slot across [0, nk).  Workgroups that
   // are resident together start near the same block index and then advance
   // through their ascending lists at about the same pace, so together they
   // sweep a narrow window of K/V blocks that stays in L2.  The softmax is
   // order independent; the order is a function of blockIdx only.
   constexpr int kResident = 128;  // workgroups resident per XCD (32 CUs x 4)
   const int slot = blockIdx.x / kNumXcd;
-  const int n0 = (int)(((int64_t)(slot % kResident) * p.nb) / kResident);
-  const int j0 = list.count_below(n0, p.g);
+  const int n0 = (int)(((int64_t)(slot % kResident) * p.nk) / kResident);
+  const int j0 = list.count_below(n0, p.gk);
   // Next valid position in rotated order after position j (j < 0: start);
   // returns top_k at the end.
   auto next_rot = [&](int j) -> int {
     if (j < 0 || j >= j0) {
-      const int r = list.next(j < 0 ? j0 : j + 1, p.g);
+      const int r = list.next(j < 0 ? j0 : j + 1, p.gk);
       if (r < p.top_k) return r;
       j = -1;
     }
-    const int r = list.next(j + 1, p.g);
+    const int r = list.next(j + 1, p.gk);
     return r < j0 ? r : p.top_k;
   };
   int j = next_rot(-1);
@@ -548,15 +548,15 @@ __global__ __launch_bounds__(256) void attn_valu_kernel(AttnParams p) {
   const float sl2 = p.scale_log2;
   const int32_t* list = p.idx + ((int64_t)bh * p.nb + qb) * p.top_k;
 
-  for (int j = next_valid(list, 0, p.top_k, p.nb); j < p.top_k;
-       j = next_valid(list, j + 1, p.top_k, p.nb)) {
-    const int32_t tok0 = block_base_token(p.g, uniform_i32(list[j]));
+  for (int j = next_valid(list, 0, p.top_k, p.nk); j < p.top_k;
+       j = next_valid(list, j + 1, p.top_k, p.nk)) {
+    const int32_t tok0 = block_base_token(p.gk, uniform_i32(list[j]));
     for (int half = 0; half < 64; half += KH) {
       __syncthreads();
       for (int i = tid; i < KH * D; i += 256) {
         const int kr = i / D;
         const int d = i - kr * D;
-        const int32_t tok = tok0 + voxel_row_offset(p.g, half + kr);
+        const int32_t tok = tok0 + voxel_row_offset(p.gk, half + kr);
         Kf[i] = to_f32(kbase[(int64_t)tok * p.k_ss + d]);
         Vf[i] = to_f32(vbase[(int64_t)tok * p.v_ss + d]);
       }

@@ -180,13 +180,15 @@ struct AttnParams {
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;
   int64_t o_sb, o_sh, o_ss;
-  const int32_t* idx;
+  const int32_t* idx;     // [B, H, nb, top_k] K/V block ids in [0, nk)
   const int32_t* order;  // [B*H*nb] launch order of q-blocks per head, or null
-  int32_t B, H, nb, top_k;
+  int32_t B, H, nb, top_k;  // nb: q-blocks per head
+  int32_t nk;               // K/V blocks per head
   float scale_log2;
   // Bytes spanned by one head of k / v (buffer-descriptor extents).
   uint32_t k_head_bytes, v_head_bytes;
-  Geom g;
+  Geom g;   // block geometry of q and out
+  Geom gk;  // block geometry of k and v (the same as g unless S_q != S_k)
 };
 
 // Chooses the MFMA kernel (fp16/bf16, D in {64,128}, scale >= 0) or the

@@ -90,11 +90,14 @@ uint64_t head_bytes(int64_t S, int64_t row_stride, int64_t D, int dtype) {
   return (uint64_t)((S - 1) * row_stride + D) * (uint64_t)elem_bytes(dtype);
 }
 
+// q / out have S rows in geometry g (nb blocks); k / v have Sk rows in
+// geometry gk (nk blocks).
 int check_attn_args(const void* q, const void* k, const void* v, const void* out, int dtype,
-                    int64_t B, int64_t H, int64_t S, int64_t D, const lcv_bsa_strides& qs,
-                    const lcv_bsa_strides& ks, const lcv_bsa_strides& vs,
-                    const lcv_bsa_strides& os, int64_t top_k, float sm_scale,
-                    const lcv_bsa_geom& g, int64_t* nb, int64_t* bs) {
+                    int64_t B, int64_t H, int64_t S, int64_t Sk, int64_t D,
+                    const lcv_bsa_strides& qs, const lcv_bsa_strides& ks,
+                    const lcv_bsa_strides& vs, const lcv_bsa_strides& os, int64_t top_k,
+                    float sm_scale, const lcv_bsa_geom& g, const lcv_bsa_geom& gk, int64_t* nb,
+                    int64_t* nk, int64_t* bs) {
   if (!q || !k || !v || !out) return fail(LCV_BSA_ERR_INVALID_ARG, "null tensor pointer");
   if (!dtype_ok(dtype)) return fail(LCV_BSA_ERR_DTYPE, "unknown dtype %d", dtype);
   int st = check_geom(B, H, S, D, g, nb, bs);
@@ -103,6 +106,12 @@ int check_attn_args(const void* q, const void* k, const void* v, const void* out
     return fail(LCV_BSA_ERR_UNSUPPORTED,
                 "block size cT*cH*cW=%lld: the attention kernels require 64-token blocks",
                 (long long)*bs);
+  int64_t bsk = 0;
+  if ((st = check_geom(B, H, Sk, D, gk, nk, &bsk))) return st;
+  if (bsk != 64)
+    return fail(LCV_BSA_ERR_UNSUPPORTED,
+                "k/v block size cT*cH*cW=%lld: the attention kernels require 64-token blocks",
+                (long long)bsk);
   if (!lcv::attn_supported(dtype, (int)D))
     return fail(LCV_BSA_ERR_UNSUPPORTED, "head_dim D=%lld unsupported (D in {16,32,64,128,256})",
                 (long long)D);
@@ -119,7 +128,7 @@ int check_attn_args(const void* q, const void* k, const void* v, const void* out
       return fail(LCV_BSA_ERR_LAYOUT,
                   "q/k/v/out rows must start on 16-byte boundaries (pointers 16-byte aligned, "
                   "strides multiples of %d elements)", vec);
-    if (head_bytes(S, ks.s, D, dtype) > 0xFFFFFFFFull || head_bytes(S, vs.s, D, dtype) > 0xFFFFFFFFull)
+    if (head_bytes(Sk, ks.s, D, dtype) > 0xFFFFFFFFull || head_bytes(Sk, vs.s, D, dtype) > 0xFFFFFFFFull)
       return fail(LCV_BSA_ERR_LAYOUT, "one head of k or v spans more than 4 GiB");
   }
   return LCV_BSA_OK;
@@ -129,8 +138,9 @@ lcv::AttnParams make_attn_params(const void* q, const void* k, const void* v, vo
                                  const lcv_bsa_strides& qs, const lcv_bsa_strides& ks,
                                  const lcv_bsa_strides& vs, const lcv_bsa_strides& os,
                                  const int32_t* idx, const int32_t* order, int64_t B, int64_t H,
-                                 int64_t S, int64_t D, int dtype, int64_t nb, int64_t top_k,
-                                 float sm_scale, const lcv_bsa_geom& g) {
+                                 int64_t Sk, int64_t D, int dtype, int64_t nb, int64_t nk,
+                                 int64_t top_k, float sm_scale, const lcv_bsa_geom& g,
+                                 const lcv_bsa_geom& gk) {
   lcv::AttnParams p{};
   p.q = q;
   p.k = k;
@@ -145,12 +155,14 @@ lcv::AttnParams make_attn_params(const void* q, const void* k, const void* v, vo
   p.B = (int32_t)B;
   p.H = (int32_t)H;
   p.nb = (int32_t)nb;
+  p.nk = (int32_t)nk;
   p.top_k = (int32_t)top_k;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
-  const uint64_t kb = head_bytes(S, ks.s, D, dtype), vb = head_bytes(S, vs.s, D, dtype);
+  const uint64_t kb = head_bytes(Sk, ks.s, D, dtype), vb = head_bytes(Sk, vs.s, D, dtype);
   p.k_head_bytes = kb > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)kb;
   p.v_head_bytes = vb > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)vb;
   p.g = lcv::make_geom(g);
+  p.gk = lcv::make_geom(gk);
   return p;
 }
 
@@ -256,13 +268,22 @@ int lcv_bsa_attn_fwd(const void* q, const void* k, const void* v, int dtype, int
                      lcv_bsa_strides vs, const int32_t* idx, const int32_t* order, int64_t top_k,
                      float sm_scale, lcv_bsa_geom g, void* out, lcv_bsa_strides os,
                      void* stream) {
-  int64_t nb = 0, bs = 0;
-  int st = check_attn_args(q, k, v, out, dtype, B, H, S, D, qs, ks, vs, os, top_k, sm_scale, g,
-                           &nb, &bs);
+  return lcv_bsa_attn_fwd_kv(q, k, v, dtype, B, H, S, S, D, qs, ks, vs, idx, order, top_k, sm_scale,
+                             g, g, out, os, stream);
+}
+
+int lcv_bsa_attn_fwd_kv(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                        int64_t H, int64_t Sq, int64_t Sk, int64_t D, lcv_bsa_strides qs,
+                        lcv_bsa_strides ks, lcv_bsa_strides vs, const int32_t* idx,
+                        const int32_t* order, int64_t top_k, float sm_scale, lcv_bsa_geom gq,
+                        lcv_bsa_geom gk, void* out, lcv_bsa_strides os, void* stream) {
+  int64_t nq = 0, nk = 0, bs = 0;
+  int st = check_attn_args(q, k, v, out, dtype, B, H, Sq, Sk, D, qs, ks, vs, os, top_k, sm_scale,
+                           gq, gk, &nq, &nk, &bs);
   if (st) return st;
   if (!idx) return fail(LCV_BSA_ERR_INVALID_ARG, "null block index pointer");
-  const lcv::AttnParams p = make_attn_params(q, k, v, out, qs, ks, vs, os, idx, order, B, H, S, D,
-                                             dtype, nb, top_k, sm_scale, g);
+  const lcv::AttnParams p = make_attn_params(q, k, v, out, qs, ks, vs, os, idx, order, B, H, Sk, D,
+                                             dtype, nq, nk, top_k, sm_scale, gq, gk);
   return launch_status(lcv::launch_attn(p, dtype, (int)D, (hipStream_t)stream),
                        "lcv_bsa_attn_fwd");
 }
@@ -284,9 +305,9 @@ int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype, int6
                     lcv_bsa_strides vs, int64_t top_k, float sm_scale, lcv_bsa_geom g,
                     void* workspace, size_t workspace_bytes, int32_t* idx, void* out,
                     lcv_bsa_strides os, void* stream) {
-  int64_t nb = 0, bs = 0;
-  int st = check_attn_args(q, k, v, out, dtype, B, H, S, D, qs, ks, vs, os, top_k, sm_scale, g,
-                           &nb, &bs);
+  int64_t nb = 0, nk = 0, bs = 0;
+  int st = check_attn_args(q, k, v, out, dtype, B, H, S, S, D, qs, ks, vs, os, top_k, sm_scale, g,
+                           g, &nb, &nk, &bs);
   if (st) return st;
   if (!idx || !workspace) return fail(LCV_BSA_ERR_INVALID_ARG, "null idx or workspace pointer");
   if (top_k > nb)
@@ -321,8 +342,8 @@ int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype, int6
     if (st) return st;
   }
   const lcv::AttnParams p = make_attn_params(q, k, v, out, qs, ks, vs, os, idx,
-                                             sched ? order : nullptr, B, H, S, D, dtype, nb,
-                                             top_k, sm_scale, g);
+                                             sched ? order : nullptr, B, H, S, D, dtype, nb, nb,
+                                             top_k, sm_scale, g, g);
   return launch_status(lcv::launch_attn(p, dtype, (int)D, s), "lcv_bsa_forward(attn)");
 }
 

@@ -269,6 +269,7 @@ def bsa_attention(
     return_indices: bool = False,
     block_means: Optional[tuple[torch.Tensor, torch.Tensor]] = None,
     out: Optional[torch.Tensor] = None,
+    kv_shape: Optional[tuple[int, int, int]] = None,
 ):
     """Block Sparse Attention forward (block_sparse_attention.py:201-250).
 
@@ -280,10 +281,15 @@ def bsa_attention(
     ``prepare_qk``) skips the pooling pass.  ``out`` is an optional
     ``[B, H, S, D]`` destination with unit last stride (e.g. a head-major
     view of a ``[B, S, H, D]`` buffer).
+
+    ``kv_shape`` extends the reference (whose layer sends S_q != S_k to dense
+    attention, attention.py:89): k and v are ``[B, H, S_k, D]`` over the
+    latent grid ``kv_shape``, cut by the same ``chunk_thw``; each q-block
+    keeps the top-k of the ``nk`` k-blocks (the count rule over ``nk``).
     """
     _require_device(q, k, v)
     q, k, v = _bhsd(q, "q"), _bhsd(k, "k"), _bhsd(v, "v")
-    if not (q.shape == k.shape == v.shape):
+    if kv_shape is None and not (q.shape == k.shape == v.shape):
         raise ValueError(f"q, k, v shapes differ: {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("q, k, v must share a dtype")
@@ -292,18 +298,28 @@ def bsa_attention(
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
     nb = num_blocks(shape, chunk_thw)
-    kk = num_selected_blocks(nb, sparsity) if top_k is None else int(top_k)
-    if not 1 <= kk <= nb:
-        raise ValueError(f"top_k={kk} must be in [1, {nb}]")
-    if block_means is not None:
-        qb, kb = block_means
-        for name, t in (("q_blocks", qb), ("k_blocks", kb)):
-            if tuple(t.shape) != (B, H, nb, D) or t.dtype != torch.float32:
-                raise ValueError(f"{name} must be fp32 [{B}, {H}, {nb}, {D}], got {tuple(t.shape)} {t.dtype}")
+    nk = nb if kv_shape is None else num_blocks(kv_shape, chunk_thw)
+    kk = num_selected_blocks(nk, sparsity) if top_k is None else int(top_k)
+    if not 1 <= kk <= nk:
+        raise ValueError(f"top_k={kk} must be in [1, {nk}]")
+    if block_means is not None or kv_shape is not None:
         from .block_sparse_attention_hip import bsa_attention_hip
 
+        if kv_shape is not None:
+            if not (k.shape == v.shape and k.shape[:2] == q.shape[:2] and k.shape[3] == D):
+                raise ValueError(f"k, v must be [B, H, S_k, D] matching q {tuple(q.shape)}: "
+                                 f"got {tuple(k.shape)}, {tuple(v.shape)}")
+            _check_shape(k.shape[2], kv_shape, chunk_thw)
+        if block_means is not None:
+            qb, kb = block_means
+            for name, t, n in (("q_blocks", qb, nb), ("k_blocks", kb, nk)):
+                if tuple(t.shape) != (B, H, n, D) or t.dtype != torch.float32:
+                    raise ValueError(f"{name} must be fp32 [{B}, {H}, {n}, {D}], got {tuple(t.shape)} {t.dtype}")
+        else:
+            qb = mean_pool_blocks_3d(q, shape, chunk_thw)
+            kb = mean_pool_blocks_3d(k, kv_shape, chunk_thw)
         idx = select_block_indices(qb, kb, kk)
-        out = bsa_attention_hip(q, k, v, idx, chunk_thw, shape, sm_scale, out=out)
+        out = bsa_attention_hip(q, k, v, idx, chunk_thw, shape, sm_scale, out=out, kv_shape=kv_shape)
         return (out, idx) if return_indices else out
     code = _dtype_code(q)
     if code != _lib.F32:

@@ -58,6 +58,7 @@ def bsa_attention_hip(
     sm_scale: Optional[float] = None,
     *,
     out: Optional[torch.Tensor] = None,
+    kv_shape: Optional[tuple[int, int, int]] = None,
 ) -> torch.Tensor:
     """Attend each q-block to the KV blocks listed in ``block_indices``.
 
@@ -73,6 +74,9 @@ def bsa_attention_hip(
             last stride and 16-byte aligned rows, e.g. the ``transpose(1, 2)``
             view of a ``[B, S, H, D]`` buffer, so the head merge after
             attention needs no copy.
+        kv_shape: the latent grid of k / v when it differs from q's (k, v
+            ``[B, H, S_k, D]``; ``block_indices`` then holds k/v block ids),
+            e.g. noise queries over conditioning + noise keys.
     Returns: ``[B, H, S, D]`` in q's dtype (``out`` when given).
     """
     if shape is None:
@@ -82,17 +86,26 @@ def bsa_attention_hip(
         )
     _require_device(q, k, v, block_indices)
     q, k, v = _bhsd(q, "q"), _bhsd(k, "k"), _bhsd(v, "v")
-    if not (q.shape == k.shape == v.shape):
-        raise ValueError("q, k, v must have the same shape")
+    if kv_shape is None:
+        if not (q.shape == k.shape == v.shape):
+            raise ValueError("q, k, v must have the same shape")
+    elif not (k.shape == v.shape and k.shape[:2] == q.shape[:2] and k.shape[3] == q.shape[3]):
+        raise ValueError(f"k, v must be [B, H, S_k, D] matching q {tuple(q.shape)}: "
+                         f"got {tuple(k.shape)}, {tuple(v.shape)}")
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("q, k, v must share a dtype")
     B, H, S, D = q.shape
+    Sk = k.shape[2]
+    kshape = tuple(shape) if kv_shape is None else tuple(kv_shape)
     BS = int(chunk_thw[0]) * int(chunk_thw[1]) * int(chunk_thw[2])
     if S % BS != 0:
         raise ValueError(f"S={S} must be a multiple of block_size={BS}.")
+    if Sk % BS != 0:
+        raise ValueError(f"S_k={Sk} must be a multiple of block_size={BS}.")
     if BS != 64:
         raise ValueError(f"the HIP BSA kernel requires block_size=64 (got {BS}).")
     _check_shape(S, shape, chunk_thw)
+    _check_shape(Sk, kshape, chunk_thw)
     nb = num_blocks(shape, chunk_thw)
     bi = block_indices
     if bi.dim() != 4 or tuple(bi.shape[:3]) != (B, H, nb):
@@ -111,11 +124,11 @@ def bsa_attention_hip(
         q, k, v = _aligned_rows(q), _aligned_rows(k), _aligned_rows(v)
     order = schedule_block_order(bi) if nb <= MAX_SCHEDULED_BLOCKS else None
     out = _output(out, q)
-    st = _lib.load().lcv_bsa_attn_fwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), code, B, H, S, D,
+    st = _lib.load().lcv_bsa_attn_fwd_kv(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), code, B, H, S, Sk, D,
         _strides(q), _strides(k), _strides(v), bi.data_ptr(),
         order.data_ptr() if order is not None else None, top_k, float(sm_scale),
-        _geom(shape, chunk_thw), out.data_ptr(), _strides(out), _stream(q),
+        _geom(shape, chunk_thw), _geom(kshape, chunk_thw), out.data_ptr(), _strides(out), _stream(q),
     )
     _lib.check(st, "bsa_attention_hip")
     return out

@@ -172,11 +172,14 @@ def block_tokens(shape, chunk_thw):
 
 def sparse_attention_from_indices(q, k, v, block_indices, shape, chunk_thw=(4, 4, 4),
                                   sm_scale=None, acc=np.float64, q_blocks=None,
-                                  heads: Optional[Sequence[tuple]] = None):
+                                  heads: Optional[Sequence[tuple]] = None, kv_shape=None):
     """Attention of each q-block over the keys of its listed KV blocks -- the
     reference kernels' contract (block_sparse_attention_metal.py:75-164:
-    entries listed twice count twice).  Entries outside [0, nb) are skipped.
+    entries listed twice count twice).  Entries outside [0, nk) are skipped.
     Equal to the masked Tier A form when the lists hold distinct valid blocks.
+
+    ``kv_shape`` (default ``shape``) is the latent grid of k / v when their
+    length differs from q's; the lists then hold k/v block ids.
 
     Returns [B,H,S,D] in ``acc`` (rows of q-blocks not computed are NaN when
     ``q_blocks`` restricts the set).  ``heads`` optionally restricts (b, h).
@@ -186,7 +189,9 @@ def sparse_attention_from_indices(q, k, v, block_indices, shape, chunk_thw=(4, 4
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
     bt = block_tokens(shape, chunk_thw)
+    btk = bt if kv_shape is None else block_tokens(kv_shape, chunk_thw)
     nb, bs = bt.shape
+    nk = btk.shape[0]
     bi = np.asarray(block_indices)
     out = np.full((B, H, S, D), np.nan, dtype=acc)
     pairs = heads if heads is not None else [(b, h) for b in range(B) for h in range(H)]
@@ -195,12 +200,12 @@ def sparse_attention_from_indices(q, k, v, block_indices, shape, chunk_thw=(4, 4
         qh, kh, vh = _f(q[b, h], acc), _f(k[b, h], acc), _f(v[b, h], acc)
         for n in qsel:
             lst = bi[b, h, n]
-            lst = lst[(lst >= 0) & (lst < nb)]
+            lst = lst[(lst >= 0) & (lst < nk)]
             tq = bt[n]
             if lst.size == 0:
                 out[b, h, tq] = 0.0
                 continue
-            keys = bt[lst].reshape(-1)
+            keys = btk[lst].reshape(-1)
             s = (qh[tq] @ kh[keys].T) * acc(sm_scale)
             s -= s.max(axis=-1, keepdims=True)
             p = np.exp(s)
@@ -210,13 +215,17 @@ def sparse_attention_from_indices(q, k, v, block_indices, shape, chunk_thw=(4, 4
 
 
 def bsa_attention(q, k, v, shape, sparsity=0.9375, chunk_thw=(4, 4, 4), sm_scale=None,
-                  top_k=None, acc=np.float64, return_indices=False):
+                  top_k=None, acc=np.float64, return_indices=False, kv_shape=None):
     """Tier A result via the block-gathered form (no S^2 mask): equal to
-    bsa_attention_masked because masked entries contribute exactly zero."""
+    bsa_attention_masked because masked entries contribute exactly zero.
+
+    ``kv_shape``: k / v over their own latent grid (S_k != S_q), pooled with
+    the same voxel; the count rule then runs over the k-blocks.  The
+    reference never routes this case through BSA (attention.py:89)."""
     qb = mean_pool_blocks_3d(q, shape, chunk_thw)
-    kb = mean_pool_blocks_3d(k, shape, chunk_thw)
+    kb = mean_pool_blocks_3d(k, shape if kv_shape is None else kv_shape, chunk_thw)
     idx, _ = topk_block_indices(block_routing_scores(qb, kb), sparsity, top_k)
-    out = sparse_attention_from_indices(q, k, v, idx, shape, chunk_thw, sm_scale, acc)
+    out = sparse_attention_from_indices(q, k, v, idx, shape, chunk_thw, sm_scale, acc, kv_shape=kv_shape)
     return (out, idx) if return_indices else out
 
 

@@ -402,3 +402,70 @@ def test_attn_wide_score_range_rescales(device, dtype, q_scale):
     out = bsa_attention_hip(q, k, v, torch.from_numpy(idx).to(device), chunk, shape)
     ref = O.sparse_attention_from_indices(_np(q), _np(k), _np(v), idx, shape, chunk)
     assert_close_report(_np(out), ref, *TOL[dtype], f"wide range q*{q_scale} {dtype}")
+
+
+# ---------------------------------------------------------------------------
+# S_q != S_k: queries over a longer (conditioning + noise) key sequence
+# ---------------------------------------------------------------------------
+
+KV_GEOMS = [
+    ((4, 8, 8), (8, 8, 8), (4, 4, 4)),          # noise frames over cond + noise frames
+    ((1, 1, 1024), (1, 1, 2560), (1, 1, 64)),   # contiguous 64-token blocks
+    ((1, 1, 256), (1, 1, 64), (1, 1, 64)),      # fewer keys than queries
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("geom", KV_GEOMS)
+def test_attn_kv_matches_oracle(device, dtype, D, geom):
+    from lcv_bsa import bsa_attention_hip
+
+    q_shape, kv_shape, chunk = geom
+    Sq, Sk = int(np.prod(q_shape)), int(np.prod(kv_shape))
+    nq, nk = Sq // 64, Sk // 64
+    q = _rand((2, 2, Sq, D), dtype, device, seed=21)
+    k, v = (_rand((2, 2, Sk, D), dtype, device, seed=s) for s in (22, 23))
+    for topk in sorted({1, min(3, nk), nk}):
+        idx = _distinct_indices(2, 2, nq, nk, topk, seed=topk + D, sort=(topk != 3))
+        out = bsa_attention_hip(q, k, v, torch.from_numpy(idx).to(device), chunk, q_shape, kv_shape=kv_shape)
+        ref = O.sparse_attention_from_indices(_np(q), _np(k), _np(v), idx, q_shape, chunk, kv_shape=kv_shape)
+        assert out.shape == q.shape
+        assert_close_report(_np(out), ref, *TOL[dtype], f"attn kv {dtype} D={D} {geom} k={topk}")
+
+
+def test_attn_kv_padding_and_out_of_range(device):
+    """Entries < 0 or >= nk are skipped; ids in [nq, nk) are real k-blocks."""
+    from lcv_bsa import bsa_attention_hip
+
+    q = _rand((1, 1, 128, 128), torch.float16, device, seed=31)
+    k, v = (_rand((1, 1, 384, 128), torch.float16, device, seed=s) for s in (32, 33))
+    idx = np.array([[[[5, -1, 4], [6, 2, -3]]]], dtype=np.int32)   # nk = 6: 6 and -3 are skipped
+    out = bsa_attention_hip(q, k, v, torch.from_numpy(idx).to(device), (1, 1, 64), (1, 1, 128),
+                            kv_shape=(1, 1, 384))
+    ref = O.sparse_attention_from_indices(_np(q), _np(k), _np(v), idx, (1, 1, 128), (1, 1, 64),
+                                          kv_shape=(1, 1, 384))
+    assert_close_report(_np(out), ref, *TOL[torch.float16], "kv padding")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_bsa_kv_end_to_end(device, dtype):
+    """bsa_attention(..., kv_shape=): the noise half of a sequence attends to
+    the whole of it.  Routing is the exact top-k of the pooled means' scores
+    (the count rule over nk), and the output matches the oracle on it."""
+    from lcv_bsa import bsa_attention
+    from lcv_bsa.block_sparse_attention import mean_pool_blocks_3d
+
+    full, noise, chunk = (8, 8, 16), (4, 8, 16), (4, 4, 4)
+    S, Sq = int(np.prod(full)), int(np.prod(noise))
+    q_all, k, v = (_rand((1, 2, S, 128), dtype, device, seed=s) for s in (41, 42, 43))
+    q = q_all[:, :, S - Sq:]
+    out, idx = bsa_attention(q, k, v, noise, sparsity=0.75, chunk_thw=chunk, return_indices=True,
+                             kv_shape=full)
+    nk = S // 64
+    assert idx.shape[-1] == max(1, int(0.25 * nk))
+    qb, kb = mean_pool_blocks_3d(q, noise, chunk), mean_pool_blocks_3d(k, full, chunk)
+    ref_idx, _ = O.topk_block_indices(O.block_routing_scores(_np(qb), _np(kb)), top_k=idx.shape[-1])
+    assert np.array_equal(idx.cpu().numpy(), ref_idx)
+    ref = O.sparse_attention_from_indices(_np(q), _np(k), _np(v), ref_idx, noise, chunk, kv_shape=full)
+    assert_close_report(_np(out), ref, *TOL[dtype], f"bsa kv {dtype}")

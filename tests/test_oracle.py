@@ -394,3 +394,52 @@ def test_prepare_qk_composes_the_pinned_steps():
     f1 = O.rope_freqs_3d((64, 1, 1), 64)
     assert np.all(f1[0] == 0.0)
     assert np.array_equal(qo1[..., 0, :], O.rms_norm_fp32(q1, None, 1e-6, "f16")[..., 0, :])
+
+
+# ---------------------------------------------------------------------------
+# S_q != S_k (queries over a longer key sequence)
+# ---------------------------------------------------------------------------
+
+def test_kv_shape_all_blocks_is_dense_over_all_keys():
+    """Noise queries (the last frames) over conditioning + noise keys: with
+    every k-block selected the gathered form is dense attention of q over
+    all of k (torch's SDPA), for voxel and contiguous geometries."""
+    rng = np.random.default_rng(5)
+    for q_shape, kv_shape, chunk in (((4, 8, 8), (8, 8, 8), (4, 4, 4)),
+                                     ((1, 1, 256), (1, 1, 448), (1, 1, 64))):
+        Sq, Sk = int(np.prod(q_shape)), int(np.prod(kv_shape))
+        q = rng.normal(size=(1, 2, Sq, 16))
+        k = rng.normal(size=(1, 2, Sk, 16))
+        v = rng.normal(size=(1, 2, Sk, 16))
+        nk = Sk // 64
+        out, idx = O.bsa_attention(q, k, v, q_shape, chunk_thw=chunk, top_k=nk, return_indices=True,
+                                   kv_shape=kv_shape)
+        assert idx.shape == (1, 2, Sq // 64, nk)
+        assert np.allclose(out, torch_sdpa(q, k, v, 0.25), atol=1e-12)
+
+
+def test_kv_shape_equal_grids_match_square_form():
+    rng = np.random.default_rng(6)
+    shape = (4, 8, 8)
+    q, k, v = (rng.normal(size=(1, 2, 256, 16)) for _ in range(3))
+    a = O.bsa_attention(q, k, v, shape, top_k=2)
+    b = O.bsa_attention(q, k, v, shape, top_k=2, kv_shape=shape)
+    assert np.array_equal(a, b)
+
+
+def test_kv_shape_routes_over_key_blocks():
+    """Each q-block keeps the top-k k-blocks of the longer key grid: plant a
+    key block that matches q-block 0 exactly and check it is selected, and
+    that k-block ids beyond nq occur (the lists index k, not q)."""
+    rng = np.random.default_rng(7)
+    Sq, Sk = 128, 320
+    q = rng.normal(size=(1, 1, Sq, 16)) * 0.1
+    k = rng.normal(size=(1, 1, Sk, 16)) * 0.1
+    v = rng.normal(size=(1, 1, Sk, 16))
+    direction = np.zeros(16)
+    direction[3] = 5.0
+    q[0, 0, :64] += direction
+    k[0, 0, 256:320] += direction            # k-block 4 (beyond nq = 2)
+    _, idx = O.bsa_attention(q, k, v, (1, 1, Sq), chunk_thw=(1, 1, 64), top_k=1, return_indices=True,
+                             kv_shape=(1, 1, Sk))
+    assert idx[0, 0, 0, 0] == 4
