@@ -297,6 +297,87 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int)
     }
 
 
+def bench_kv_split(lib, dev, stream, steps: int, warmup: int, seed: int):
+    """BSA where queries and keys differ in length: the noise queries of a
+    720p continuation (16 noise latent frames after 4 conditioning frames)
+    over all 20 frames' keys -- the case the reference sends to dense
+    attention (attention.py:218-221).  B=1, 32 heads, D=128, fp16, 64-token
+    blocks: nq = 900 q-blocks over nk = 1125 k-blocks, top-k 71
+    (ceil(0.0625 * 1125)).  Synthetic inputs as the headline workload's, with
+    RoPE on the full (20, 45, 80) grid."""
+    import torch
+
+    from lcv_bsa import _lib
+    from lcv_bsa.block_sparse_attention import (
+        _geom, _strides, bsa_attention, mean_pool_blocks_3d, select_block_indices,
+    )
+    from lcv_bsa.block_sparse_attention_hip import schedule_block_order
+    from lcv_bsa.workloads import make_inputs
+
+    grid, ncl, H, D, top_k = (20, 45, 80), 4, 32, 128, 71
+    Sk = grid[0] * grid[1] * grid[2]
+    nc = ncl * grid[1] * grid[2]
+    Sq = Sk - nc
+    q_all, k, v, _ = make_inputs(1, H, D, (1, 1, Sk), (1, 1, 64), torch.float16, dev, seed=seed + 4, grid=grid)
+    q = q_all[:, :, nc:]
+    qshape, kshape, chunk = (1, 1, Sq), (1, 1, Sk), (1, 1, 64)
+    idx = select_block_indices(mean_pool_blocks_3d(q, qshape, chunk), mean_pool_blocks_3d(k, kshape, chunk), top_k)
+    order = schedule_block_order(idx)
+    out = torch.empty_like(q)
+    sh = stream.cuda_stream
+    scale = 1.0 / math.sqrt(D)
+
+    def attn():
+        _lib.check(lib.lcv_bsa_attn_fwd_kv(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.F16, 1, H, Sq, Sk, D, _strides(q), _strides(k),
+            _strides(v), idx.data_ptr(), order.data_ptr(), top_k, scale, _geom(qshape, chunk), _geom(kshape, chunk),
+            out.data_ptr(), _strides(out), sh), "attn_fwd_kv")
+
+    def full():
+        bsa_attention(q, k, v, qshape, chunk_thw=chunk, sm_scale=scale, top_k=top_k, kv_shape=kshape)
+
+    def timed(fn, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    for _ in range(warmup):
+        attn()
+        full()
+    ms_attn = timed(attn, steps)
+    ms_full = timed(full, steps)
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    def dense():
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale)
+    try:
+        dense()
+        ms_dense = timed(dense, 2)
+    except RuntimeError as e:  # no fused SDPA kernel for this shape
+        log(f"dense SDPA unavailable: {e}")
+        ms_dense = None
+    flop = 4 * H * (Sq // 64) * top_k * 64 * 64 * D
+    tflops = flop / (ms_attn * 1e-3) / 1e12
+    del q_all, k, v, out
+    torch.cuda.empty_cache()
+    return {
+        "workload": "720p continuation: noise queries (16 latent frames, 57600 tokens) over 4 conditioning + 16 "
+                    "noise frames of keys (72000 tokens), B1 H32 D128 fp16, 64-token blocks, top-k 71 of 1125",
+        "ms_attention": round(ms_attn, 4),
+        "executed_tflop": round(flop / 1e12, 4),
+        "achieved": round(tflops, 1),
+        "frac_of_2500": round(tflops / 2500.0, 4),
+        "ms_total": round(ms_full, 4),
+        "dense_sdpa_ms": None if ms_dense is None else round(ms_dense, 3),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -309,6 +390,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prepare", action="store_true", help="skip the pre-BSA prepare_qk timing")
     ap.add_argument("--no-dit-block", action="store_true", help="skip the 720p DiT block timing")
+    ap.add_argument("--no-kv-split", action="store_true", help="skip the S_q != S_k (continuation) timing")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (a known-size kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -466,6 +548,11 @@ def main() -> int:
         result["pre_bsa"] = pre
         log(f"pre-BSA prepare_qk {pre['ms']:.3f} ms ({pre['achieved']:.0f} GB/s, "
             f"{100 * pre['frac']:.1f}% of HBM); unfused torch chain {pre['unfused_torch_ms']:.3f} ms")
+    if args.config == "c2" and not args.no_kv_split:
+        kv = bench_kv_split(lib, dev, stream, args.steps, args.warmup, args.seed)
+        result["kv_split"] = kv
+        log(f"S_q != S_k (continuation): attention {kv['ms_attention']:.3f} ms ({kv['achieved']:.0f} TFLOP/s, "
+            f"{100 * kv['frac_of_2500']:.1f} %), pipeline {kv['ms_total']:.3f} ms; dense SDPA {kv['dense_sdpa_ms']} ms")
     if args.config == "c2" and not args.no_dit_block:
         blk = bench_dit_block(dev, stream, max(3, args.steps // 2), 2, args.seed, top_k)
         result["dit_block"] = blk

@@ -10,8 +10,9 @@ those means, writing straight into the ``[B, N, H, D]`` layout the output
 projection reads.  AdaLN modulation and the gated residuals stay in fp32 as
 in the reference.
 
-Scope: the text-to-video block (no KV cache, no conditioning latents); the
-cross-attention handles any batch with per-item text lengths.
+The block covers the reference's paths: text-to-video, conditioning latents
+(image-to-video / continuation), returning the KV cache and continuing from
+it; the cross-attention handles any batch with per-item text lengths.
 """
 
 from __future__ import annotations
@@ -93,16 +94,23 @@ class FeedForwardSwiGLU(nn.Module):
 
 
 class Attention(nn.Module, BSAAttention):
-    """Self-attention with 3D RoPE and the BSA dispatch (attention.py:40-233,
-    text-to-video path).
+    """Self-attention with 3D RoPE and the BSA dispatch (attention.py:40-276):
+    the plain path, the conditioning split (``num_cond_latents``) and the
+    KV-cache continuation.
 
-    With BSA on, the geometry comes from ``bsa_shape_policy`` (``"reference"``
-    keeps the reference's dense fallback when the voxel does not tile the
-    grid; ``"auto"`` / ``"contiguous"`` use 64-token runs instead).  The BSA
-    path is one ``prepare_qk`` over the strided q / k views of the QKV output
-    plus ``bsa_attention`` from the fused block means; a ``ValueError`` from
-    it falls back to the unfused layer and dense attention, as the reference
-    does."""
+    BSA geometry comes from ``bsa_shape_policy`` (``"reference"`` keeps the
+    reference's dense fallback when the voxel does not tile the grid;
+    ``"auto"`` / ``"contiguous"`` use 64-token runs instead).  Where queries
+    and keys differ in length -- the noise queries over conditioning + noise
+    keys (attention.py:218-221) and the KV-cache continuation (273) -- the
+    reference always runs dense attention; ``bsa_cond_noise = True`` runs BSA
+    there too (k-blocks over the longer key grid).
+
+    With BSA on and no KV cache to return, q and k go through one
+    ``prepare_qk`` over the strided views of the QKV output (RMSNorm + RoPE +
+    block means), and the attention writes straight into the ``[B, N, H, D]``
+    layout of the output projection.  A ``ValueError`` anywhere on that path
+    falls back to the reference's unfused sequence."""
 
     def __init__(self, dim: int, num_heads: int, **kw):
         nn.Module.__init__(self)
@@ -112,39 +120,116 @@ class Attention(nn.Module, BSAAttention):
         self.k_norm = RMSNorm_FP32(self.head_dim, eps=1e-6, **kw)
         self.proj = nn.Linear(dim, dim, **kw)
         self.bsa_shape_policy: str = "reference"
-        self.keep_indices: bool = False          # store the last routing (tests)
-        self.last_indices: Optional[torch.Tensor] = None
+        self.bsa_cond_noise: bool = False
+        self.keep_indices: bool = False          # store the last routing per branch (tests)
+        self.last_indices: dict = {}
+        self.last_paths: dict = {}
 
-    def _bsa(self, q, k, v, shape, geom):
-        bshape, bchunk = geom
-        B, H, N, D = q.shape
-        qp, kp, qb, kb = prepare_qk(q, k, shape, q_weight=self.q_norm.weight, k_weight=self.k_norm.weight,
-                                    eps=self.q_norm.eps, shape=bshape, chunk_thw=bchunk)
-        o = torch.empty((B, N, H, D), dtype=q.dtype, device=q.device)
-        _, idx = bsa_attention(qp, kp, v, bshape, sparsity=self.bsa_sparsity, chunk_thw=bchunk,
-                               sm_scale=self.scale, top_k=self.bsa_top_k, return_indices=True,
-                               block_means=(qb, kb), out=o.transpose(1, 2))
-        self.last_indices = idx if self.keep_indices else None
+    def _attend(self, name, q, k, v, q_shape, kv_shape=None, means=None, out=None):
+        """BSA over the policy's geometry for ``q_shape`` (and ``kv_shape``
+        when k / v are longer), else dense; writes into ``out`` if given."""
+        path = "dense"
+        if self.enable_bsa and q_shape is not None and (kv_shape is None or self.bsa_cond_noise):
+            validate_backend(self.bsa_backend)
+            gq = bsa_geometry(q_shape, self.bsa_chunk_thw, self.bsa_shape_policy)
+            gk = gq if kv_shape is None else bsa_geometry(kv_shape, self.bsa_chunk_thw, self.bsa_shape_policy)
+            if gq is not None and gk is not None and gq[1] == gk[1]:
+                try:
+                    o, idx = bsa_attention(q, k, v, gq[0], sparsity=self.bsa_sparsity, chunk_thw=gq[1],
+                                           sm_scale=self.scale, top_k=self.bsa_top_k, return_indices=True,
+                                           block_means=means, out=out,
+                                           kv_shape=None if kv_shape is None else gk[0])
+                    if self.keep_indices:
+                        self.last_indices[name] = idx
+                    path = "bsa"
+                except ValueError:
+                    pass
+        if path == "dense":
+            o = dense_attention(q, k, v, self.scale)
+            if out is not None:
+                out.copy_(o)
+                o = out
+        self.last_paths[name] = path
+        self.last_path = path
         return o
 
-    def forward(self, x: torch.Tensor, shape: Sequence[int]) -> torch.Tensor:
+    def _split(self, q, k, v, shape, ncl, o):
+        """The conditioning split (attention.py:202-221) into ``o`` [B, N, H, D]."""
+        T, Hl, Wl = (int(s) for s in shape)
+        nc = q.shape[2] // T * ncl
+        self._attend("cond", q[:, :, :nc], k[:, :, :nc], v[:, :, :nc], (ncl, Hl, Wl),
+                     out=o[:, :nc].transpose(1, 2))
+        self._attend("noise", q[:, :, nc:], k, v, (T - ncl, Hl, Wl), kv_shape=(T, Hl, Wl),
+                     out=o[:, nc:].transpose(1, 2))
+
+    def forward(self, x: torch.Tensor, shape: Sequence[int], num_cond_latents: Optional[int] = None,
+                return_kv: bool = False):
         B, N, C = x.shape
-        qkv = self.qkv(x).view(B, N, 3, self.num_heads, self.head_dim)
+        H, D = self.num_heads, self.head_dim
+        ncl = int(num_cond_latents or 0)
+        self.last_indices, self.last_paths = {}, {}
+        qkv = self.qkv(x).view(B, N, 3, H, D)
         q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
-        if self.enable_bsa and shape is not None:
+        o = torch.empty((B, N, H, D), dtype=x.dtype, device=x.device)
+        if self.enable_bsa and shape is not None and not return_kv:
             validate_backend(self.bsa_backend)
             geom = bsa_geometry(shape, self.bsa_chunk_thw, self.bsa_shape_policy)
             if geom is not None:
                 try:
-                    o = self._bsa(q, k, v, shape, geom)
-                    self.last_path = "bsa"
+                    qp, kp, qb, kb = prepare_qk(q, k, shape, q_weight=self.q_norm.weight,
+                                                k_weight=self.k_norm.weight, eps=self.q_norm.eps,
+                                                shape=geom[0], chunk_thw=geom[1])
+                    if ncl > 0:
+                        self._split(qp, kp, v, shape, ncl, o)
+                    else:
+                        self._attend("all", qp, kp, v, shape, means=(qb, kb), out=o.transpose(1, 2))
                     return self.proj(o.view(B, N, C))
                 except ValueError:
-                    pass
-        # The reference's sequence: norms, RoPE, then its BSA-or-dense dispatch.
-        q, k = rope_3d(self.q_norm(q), self.k_norm(k), tuple(shape))
-        o = self._process_attn(q, k, v, shape=shape)
-        return self.proj(o.transpose(1, 2).reshape(B, N, C))
+                    self.last_indices, self.last_paths = {}, {}
+        # The reference's sequence: norms, (cache,) RoPE, then BSA-or-dense.
+        q, k = self.q_norm(q), self.k_norm(k)
+        cache = (k, v)
+        q, k = rope_3d(q, k, tuple(shape))
+        if ncl > 0:
+            self._split(q, k, v, shape, ncl, o)
+        else:
+            self._attend("all", q, k, v, shape, out=o.transpose(1, 2))
+        out = self.proj(o.view(B, N, C))
+        return (out, cache) if return_kv else out
+
+    def forward_with_kv_cache(self, x: torch.Tensor, shape: Sequence[int], num_cond_latents: Optional[int],
+                              kv_cache: tuple) -> torch.Tensor:
+        """Chunked continuation (attention.py:235-275): fresh k / v appended to
+        the cached (normed, un-rotated) ones; with conditioning latents RoPE
+        runs over the extended grid (q zero-padded to align positions); the
+        noise queries then attend to all keys."""
+        B, N, C = x.shape
+        H, D = self.num_heads, self.head_dim
+        qkv = self.qkv(x).view(B, N, 3, H, D)
+        q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+        q, k = self.q_norm(q), self.k_norm(k)
+        T, Hl, Wl = (int(s) for s in shape)
+        k_cache, v_cache = kv_cache
+        if k_cache.shape[0] == 1 and B > 1:
+            k_cache = k_cache.expand(B, *k_cache.shape[1:])
+            v_cache = v_cache.expand(B, *v_cache.shape[1:])
+        k_full = torch.cat([k_cache, k], dim=2)
+        v_full = torch.cat([v_cache, v], dim=2)
+        ncl = int(num_cond_latents or 0)
+        if ncl > 0:
+            q_pad = torch.cat([torch.zeros_like(k_cache), q], dim=2)
+            q_pad, k_full = rope_3d(q_pad, k_full, (T + ncl, Hl, Wl))
+            q = q_pad[:, :, -N:]
+        self.last_indices, self.last_paths = {}, {}
+        Tk = k_full.shape[2] // (Hl * Wl)
+        o = torch.empty((B, N, H, D), dtype=x.dtype, device=x.device)
+        kv_shape = (Tk, Hl, Wl) if Tk * Hl * Wl == k_full.shape[2] else None
+        if kv_shape is None:
+            o.transpose(1, 2).copy_(dense_attention(q, k_full, v_full, self.scale))
+            self.last_path = self.last_paths["noise"] = "dense"
+        else:
+            self._attend("noise", q, k_full, v_full, (T, Hl, Wl), kv_shape=kv_shape, out=o.transpose(1, 2))
+        return self.proj(o.view(B, N, C))
 
 
 class MultiHeadCrossAttention(nn.Module):
@@ -164,7 +249,19 @@ class MultiHeadCrossAttention(nn.Module):
         self.q_norm = RMSNorm_FP32(self.head_dim, eps=1e-6, **kw)
         self.k_norm = RMSNorm_FP32(self.head_dim, eps=1e-6, **kw)
 
-    def forward(self, x: torch.Tensor, cond: torch.Tensor, kv_seqlen: Sequence[int]) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, cond: torch.Tensor, kv_seqlen: Sequence[int],
+                num_cond_latents: Optional[int] = None, shape: Optional[Sequence[int]] = None) -> torch.Tensor:
+        """With conditioning latents only the noise tokens attend to the text;
+        the conditioning rows of the result are zero (attention.py:355-371)."""
+        if num_cond_latents:
+            assert shape is not None
+            B, N, C = x.shape
+            nc = N // int(shape[0]) * int(num_cond_latents)
+            out_noise = self._cross(x[:, nc:], cond, kv_seqlen)
+            return torch.cat([out_noise.new_zeros((B, nc, C)), out_noise], dim=1)
+        return self._cross(x, cond, kv_seqlen)
+
+    def _cross(self, x: torch.Tensor, cond: torch.Tensor, kv_seqlen: Sequence[int]) -> torch.Tensor:
         B, N, C = x.shape
         H, D = self.num_heads, self.head_dim
         q = self.q_norm(self.q_linear(x).view(B, N, H, D)).transpose(1, 2).contiguous()
@@ -196,9 +293,11 @@ class LongCatSingleStreamBlock(nn.Module):
         self.ffn = FeedForwardSwiGLU(hidden_size, int(hidden_size * mlp_ratio), **kw)
 
     def forward(self, x: torch.Tensor, y: torch.Tensor, t: torch.Tensor, y_seqlen: Sequence[int],
-                latent_shape: Sequence[int]) -> torch.Tensor:
+                latent_shape: Sequence[int], num_cond_latents: Optional[int] = None, return_kv: bool = False,
+                kv_cache: Optional[tuple] = None, skip_crs_attn: bool = False):
         """x [B, N, C] visual tokens, y [1, sum(y_seqlen), C] packed text,
-        t [B, T, C_t] fp32 timestep embedding, latent_shape (T, H, W)."""
+        t [B, T, C_t] fp32 timestep embedding, latent_shape (T, H, W).
+        Returns x, or (x, kv) with ``return_kv`` (longcat_video_dit.py:80-138)."""
         dtype = x.dtype
         B, N, C = x.shape
         T = int(latent_shape[0])
@@ -207,11 +306,21 @@ class LongCatSingleStreamBlock(nn.Module):
         shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = ada.chunk(6, dim=-1)
 
         x_m = modulate_fp32(self.mod_norm_attn, x.view(B, T, -1, C), shift_msa, scale_msa).view(B, N, C)
-        x_s = self.attn(x_m, latent_shape)
+        new_kv = None
+        if kv_cache is not None:
+            x_s = self.attn.forward_with_kv_cache(x_m, latent_shape, num_cond_latents, kv_cache)
+            new_kv = kv_cache
+        elif return_kv:
+            x_s, new_kv = self.attn(x_m, latent_shape, num_cond_latents, return_kv=True)
+        else:
+            x_s = self.attn(x_m, latent_shape, num_cond_latents)
         x = (x.float() + (gate_msa * x_s.view(B, T, -1, C).float()).view(B, N, C)).to(dtype)
 
-        x = x + self.cross_attn(self.pre_crs_attn_norm(x), y, y_seqlen)
+        if not skip_crs_attn:
+            ncl_cross = None if kv_cache is not None else num_cond_latents
+            x = x + self.cross_attn(self.pre_crs_attn_norm(x), y, y_seqlen, ncl_cross, latent_shape)
 
         x_m = modulate_fp32(self.mod_norm_ffn, x.view(B, T, -1, C), shift_mlp, scale_mlp).view(B, N, C)
         x_s = self.ffn(x_m)
-        return (x.float() + (gate_mlp * x_s.view(B, T, -1, C).float()).view(B, N, C)).to(dtype)
+        x = (x.float() + (gate_mlp * x_s.view(B, T, -1, C).float()).view(B, N, C)).to(dtype)
+        return (x, new_kv) if return_kv else x

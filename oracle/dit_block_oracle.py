@@ -7,9 +7,9 @@ Restates ``LongCatSingleStreamBlock.__call__`` (longcat_video/models/
 longcat_video_dit.py:80-138) with its parts: ``LayerNorm_FP32`` and
 ``modulate_fp32`` (blocks.py:79-119), ``RMSNorm_FP32`` (blocks.py:55-72, in
 bsa_oracle), ``FeedForwardSwiGLU`` (blocks.py:23-51), the self-attention
-layer (attention.py:186-233, no cond/noise split) with BSA through
-bsa_oracle, and ``MultiHeadCrossAttention`` (attention.py:282-371, one batch
-item, so the block-diagonal text mask is all zeros).
+layer (attention.py:186-233, with the conditioning split of 202-221) with
+BSA through bsa_oracle, and ``MultiHeadCrossAttention`` (attention.py:
+282-371, one batch item, so the block-diagonal text mask is all zeros).
 
 Numerics follow the reference's dtypes: tensors between modules hold the
 model dtype (``round_to`` after every op that produces one), the AdaLN
@@ -28,7 +28,8 @@ from . import bsa_oracle as B
 
 __all__ = [
     "silu", "swiglu_hidden_dim", "layer_norm_fp32", "modulate_fp32", "linear", "feed_forward_swiglu",
-    "dense_attention", "self_attention", "cross_attention", "dit_block", "block_param_shapes",
+    "dense_attention", "self_attention", "self_attention_kv_cache", "cross_attention", "dit_block",
+    "block_param_shapes",
 ]
 
 F32 = np.float32
@@ -99,12 +100,34 @@ def dense_attention(q, k, v, scale: float):
     return (p / p.sum(-1, keepdims=True)) @ v
 
 
-def self_attention(x, p, latent_shape, num_heads: int, dtype: str, bsa: dict, block_indices=None):
-    """Attention.__call__ without the cond split (attention.py:186-233): fused
-    QKV, q_norm / k_norm, rope_3d over the latent grid, BSA (attention.py:
-    89-179 with the given geometry), head merge, proj.  ``bsa`` holds
-    ``shape``, ``chunk_thw`` and ``top_k``; ``block_indices`` (if given)
-    replaces the top-k routing.  Returns (out, block_indices)."""
+def _branch(q, k, v, geom, kv_geom, top_k, idx):
+    """One attention call of the layer: BSA over ``geom`` = (shape, chunk)
+    (k / v over ``kv_geom`` when they are longer; routing ``idx`` if given,
+    else the top-k of the pooled means), or dense attention when ``geom`` is
+    None.  Returns (out, idx)."""
+    D = q.shape[-1]
+    if geom is None:
+        return dense_attention(q, k, v, D ** -0.5), None
+    shape, chunk = geom
+    kv_shape = None if kv_geom is None else kv_geom[0]
+    if idx is None:
+        qb = B.mean_pool_blocks_3d(q, shape, chunk)
+        kb = B.mean_pool_blocks_3d(k, shape if kv_shape is None else kv_shape, chunk)
+        idx, _ = B.topk_block_indices(B.block_routing_scores(qb, kb), top_k=top_k)
+    return B.sparse_attention_from_indices(q, k, v, idx, shape, chunk, D ** -0.5, kv_shape=kv_shape), idx
+
+
+def self_attention(x, p, latent_shape, num_heads: int, dtype: str, bsa: dict, block_indices=None,
+                   num_cond_latents: int = 0):
+    """Attention.__call__ (attention.py:186-233): fused QKV, q_norm / k_norm,
+    rope_3d over the latent grid, then either one attention over all tokens
+    (``bsa["all"]``) or, with conditioning latents, the split of attention.py:
+    202-221: the conditioning tokens among themselves (``bsa["cond"]``) and
+    the noise queries over all keys (``bsa["noise"]`` = (q geometry, k/v
+    geometry), dense in the reference).  Each ``bsa`` entry is a
+    (shape, chunk) geometry or None for dense; ``bsa["top_k"]`` is the count.
+    ``block_indices`` maps branch name -> routing to use.  Returns (out,
+    {branch: routing})."""
     Bsz, N, C = x.shape
     H, D = num_heads, C // num_heads
     qkv = linear(x, p["attn.qkv.weight"], p["attn.qkv.bias"], dtype).reshape(Bsz, N, 3, H, D)
@@ -115,20 +138,62 @@ def self_attention(x, p, latent_shape, num_heads: int, dtype: str, bsa: dict, bl
     cos, sin = np.cos(f), np.sin(f)
     q = B.round_to(q * cos + B.rotate_half(q) * sin, dtype)
     k = B.round_to(k * cos + B.rotate_half(k) * sin, dtype)
-    if block_indices is None:
-        qb = B.mean_pool_blocks_3d(q, bsa["shape"], bsa["chunk_thw"])
-        kb = B.mean_pool_blocks_3d(k, bsa["shape"], bsa["chunk_thw"])
-        block_indices, _ = B.topk_block_indices(B.block_routing_scores(qb, kb), top_k=bsa["top_k"])
-    o = B.sparse_attention_from_indices(q, k, v, block_indices, bsa["shape"], bsa["chunk_thw"], D ** -0.5)
+    given = block_indices or {}
+    idx = {}
+    if num_cond_latents:
+        nc = N // latent_shape[0] * num_cond_latents
+        oc, idx["cond"] = _branch(q[:, :, :nc], k[:, :, :nc], v[:, :, :nc], bsa.get("cond"), None,
+                                  bsa["top_k"], given.get("cond"))
+        gq, gk = bsa.get("noise") or (None, None)
+        on, idx["noise"] = _branch(q[:, :, nc:], k, v, gq, gk, bsa["top_k"], given.get("noise"))
+        o = np.concatenate([oc, on], axis=2)
+    else:
+        o, idx["all"] = _branch(q, k, v, bsa.get("all"), None, bsa["top_k"], given.get("all"))
     o = _r(o, dtype)
     o = np.transpose(o, (0, 2, 1, 3)).reshape(Bsz, N, C)
-    return linear(o, p["attn.proj.weight"], p["attn.proj.bias"], dtype), block_indices
+    return linear(o, p["attn.proj.weight"], p["attn.proj.bias"], dtype), idx
 
 
-def cross_attention(x, y, p, num_heads: int, dtype: str):
-    """MultiHeadCrossAttention._process_cross_attn (attention.py:300-341) for
-    one batch item (x [1, N, C], text y [1, L, C]): q / kv projections,
-    q_norm / k_norm, dense attention, proj."""
+def self_attention_kv_cache(x, p, latent_shape, num_heads: int, dtype: str, kv_cache, num_cond_latents: int,
+                            bsa: dict, block_indices=None):
+    """Attention.forward_with_kv_cache (attention.py:235-275): fresh q / k / v
+    of the current chunk, k / v appended to the cache (normed, not rotated);
+    with conditioning latents RoPE runs over the extended grid with q
+    zero-padded at the cache positions; then the queries attend to all keys
+    (``bsa["noise"]`` geometry pair, or None = dense as in the reference).
+    Returns (out, {"noise": routing})."""
+    Bsz, N, C = x.shape
+    H, D = num_heads, C // num_heads
+    qkv = linear(x, p["attn.qkv.weight"], p["attn.qkv.bias"], dtype).reshape(Bsz, N, 3, H, D)
+    q, k, v = (np.transpose(qkv[:, :, i], (0, 2, 1, 3)) for i in range(3))
+    q = B.rms_norm_fp32(q, p["attn.q_norm.weight"], 1e-6, dtype)
+    k = B.rms_norm_fp32(k, p["attn.k_norm.weight"], 1e-6, dtype)
+    k_cache, v_cache = (np.asarray(a, F32) for a in kv_cache)
+    k_full = np.concatenate([k_cache, k], axis=2)
+    v_full = np.concatenate([v_cache, v], axis=2)
+    if num_cond_latents:
+        T, Hl, Wl = latent_shape
+        q_pad = np.concatenate([np.zeros_like(k_cache), q], axis=2)
+        f = B.rope_freqs_3d((T + num_cond_latents, Hl, Wl), D).astype(F32)
+        cos, sin = np.cos(f), np.sin(f)
+        q_pad = B.round_to(q_pad * cos + B.rotate_half(q_pad) * sin, dtype)
+        k_full = B.round_to(k_full * cos + B.rotate_half(k_full) * sin, dtype)
+        q = q_pad[:, :, -N:]
+    gq, gk = bsa.get("noise") or (None, None)
+    o, idx = _branch(q, k_full, v_full, gq, gk, bsa["top_k"], (block_indices or {}).get("noise"))
+    o = np.transpose(_r(o, dtype), (0, 2, 1, 3)).reshape(Bsz, N, C)
+    return linear(o, p["attn.proj.weight"], p["attn.proj.bias"], dtype), {"noise": idx}
+
+
+def cross_attention(x, y, p, num_heads: int, dtype: str, num_cond_latents: int = 0, latent_shape=None):
+    """MultiHeadCrossAttention (attention.py:300-371) for one batch item (x
+    [1, N, C], text y [1, L, C]): q / kv projections, q_norm / k_norm, dense
+    attention, proj.  With conditioning latents only the noise tokens attend
+    and the conditioning rows are zero."""
+    if num_cond_latents:
+        nc = x.shape[1] // latent_shape[0] * num_cond_latents
+        out = cross_attention(x[:, nc:], y, p, num_heads, dtype)
+        return np.concatenate([np.zeros((x.shape[0], nc, x.shape[2]), F32), out], axis=1)
     Bsz, N, C = x.shape
     H, D = num_heads, C // num_heads
     q = linear(x, p["cross_attn.q_linear.weight"], p["cross_attn.q_linear.bias"], dtype).reshape(Bsz, N, H, D)
@@ -144,11 +209,11 @@ def cross_attention(x, y, p, num_heads: int, dtype: str):
 
 
 def dit_block(x, y, t, p, latent_shape: Sequence[int], num_heads: int, dtype: str, bsa: dict,
-              block_indices=None):
-    """LongCatSingleStreamBlock.__call__ (longcat_video_dit.py:80-138), no KV
-    cache, no cond latents, cross-attention on.  x [B, N, C] (model dtype),
-    y [1, L, C] text, t [B, T, Ct] fp32 timestep embedding.  Returns
-    (x_out, block_indices of the self-attention)."""
+              block_indices=None, num_cond_latents: int = 0):
+    """LongCatSingleStreamBlock.__call__ (longcat_video_dit.py:80-138) without
+    a KV cache, cross-attention on.  x [B, N, C] (model dtype), y [1, L, C]
+    text, t [B, T, Ct] fp32 timestep embedding; ``bsa`` / ``block_indices``
+    as in ``self_attention``.  Returns (x_out, routing per branch)."""
     x = np.asarray(x, F32)
     Bsz, N, C = x.shape
     T = latent_shape[0]
@@ -158,12 +223,13 @@ def dit_block(x, y, t, p, latent_shape: Sequence[int], num_heads: int, dtype: st
     shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = np.split(ada, 6, axis=-1)
 
     x_m = modulate_fp32(x.reshape(Bsz, T, -1, C), shift_msa, scale_msa, dtype).reshape(Bsz, N, C)
-    x_s, idx = self_attention(x_m, p, latent_shape, num_heads, dtype, bsa, block_indices)
+    x_s, idx = self_attention(x_m, p, latent_shape, num_heads, dtype, bsa, block_indices, num_cond_latents)
     x = _r(x.astype(np.float64) + (gate_msa.astype(np.float64) * x_s.reshape(Bsz, T, -1, C)).reshape(Bsz, N, C),
            dtype)
 
     xn = _r(layer_norm_fp32(x, p["pre_crs_attn_norm.weight"], p["pre_crs_attn_norm.bias"]), dtype)
-    x = _r(x.astype(np.float64) + cross_attention(xn, y, p, num_heads, dtype), dtype)
+    x = _r(x.astype(np.float64) + cross_attention(xn, y, p, num_heads, dtype, num_cond_latents, latent_shape),
+           dtype)
 
     x_m = modulate_fp32(x.reshape(Bsz, T, -1, C), shift_mlp, scale_mlp, dtype).reshape(Bsz, N, C)
     x_s = feed_forward_swiglu(x_m, p["ffn.w1.weight"], p["ffn.w2.weight"], p["ffn.w3.weight"], dtype)

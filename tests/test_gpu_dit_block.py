@@ -71,13 +71,12 @@ def test_block_matches_oracle(device, policy, grid, chunk):
     with torch.no_grad():
         out = blk(x, y, t, [L], grid)
     assert blk.attn.last_path == "bsa"
-    idx = blk.attn.last_indices.cpu().numpy()
+    idx = blk.attn.last_indices["all"].cpu().numpy()
     from lcv_bsa.shape_policy import bsa_geometry
 
-    bshape, bchunk = bsa_geometry(grid, chunk, policy)
     p = {k: _np(v) for k, v in blk.state_dict().items()}
     ref, _ = DB.dit_block(_np(x), _np(y), _np(t), p, grid, H, "bf16",
-                          dict(shape=bshape, chunk_thw=bchunk, top_k=3), block_indices=idx)
+                          {"all": bsa_geometry(grid, chunk, policy), "top_k": 3}, block_indices={"all": idx})
     _check(_np(out), ref, f"block {policy} {grid}")
     assert idx.shape == (1, H, N // 64, 3) and np.all(np.diff(idx, axis=-1) > 0)
 
@@ -94,9 +93,8 @@ def test_block_reference_policy_falls_back_to_dense(device):
         out = blk(x, y, t, [L], grid)
     assert blk.attn.last_path == "dense"
     p = {k: _np(v) for k, v in blk.state_dict().items()}
-    nb = N // 64        # every block selected == dense attention
-    ref, _ = DB.dit_block(_np(x), _np(y), _np(t), p, grid, H, "bf16",
-                          dict(shape=(1, 1, N), chunk_thw=(1, 1, 64), top_k=nb))
+    nb = N // 64
+    ref, _ = DB.dit_block(_np(x), _np(y), _np(t), p, grid, H, "bf16", {"all": None, "top_k": nb})
     _check(_np(out), ref, "dense fallback")
 
 
@@ -138,3 +136,84 @@ def test_block_720p_adaln_zero_is_identity(device):
     torch.cuda.synchronize()
     assert blk.attn.last_path == "bsa"
     assert torch.equal(out, x)
+
+
+# ---------------------------------------------------------------------------
+# Conditioning split and KV-cache continuation (S_q != S_k on the noise side)
+# ---------------------------------------------------------------------------
+
+def _attn_params(blk):
+    return {"attn." + k: _np(v) for k, v in blk.attn.state_dict().items()}
+
+
+def _split_geoms(grid, ncl, chunk, policy, cond_noise, top_k):
+    from lcv_bsa.shape_policy import bsa_geometry
+
+    T, Hl, Wl = grid
+    cond, noise = (ncl, Hl, Wl), (T - ncl, Hl, Wl)
+    return {"cond": bsa_geometry(cond, chunk, policy),
+            "noise": (bsa_geometry(noise, chunk, policy), bsa_geometry(grid, chunk, policy)) if cond_noise else None,
+            "top_k": top_k}
+
+
+def _idx(blk):
+    return {k: v.cpu().numpy() for k, v in blk.attn.last_indices.items()}
+
+
+@pytest.mark.parametrize("policy,chunk,cond_noise", [
+    ("reference", (4, 4, 4), False),      # the reference: cond via BSA, noise dense
+    ("reference", (4, 4, 4), True),       # noise queries over all keys via BSA (kv geometry)
+    ("contiguous", (4, 4, 4), True),
+])
+def test_attention_cond_split_matches_oracle(device, policy, chunk, cond_noise):
+    C, H, grid, ncl = 256, 2, (8, 8, 16), 4
+    N = int(np.prod(grid))
+    blk = _block(C, H, 64, device, seed=7)
+    a = blk.attn
+    a.enable_bsa, a.bsa_chunk_thw, a.bsa_shape_policy = True, chunk, policy
+    a.bsa_cond_noise, a.bsa_top_k, a.keep_indices = cond_noise, 3, True
+    x, _, _ = _inputs(N, C, grid[0], 64, 8, device, seed=8)
+    with torch.no_grad():
+        out = a(x, grid, ncl)
+    assert a.last_paths == {"cond": "bsa", "noise": "bsa" if cond_noise else "dense"}
+    idx = _idx(blk)
+    ref, _ = DB.self_attention(_np(x), _attn_params(blk), grid, H, "bf16",
+                               _split_geoms(grid, ncl, chunk, policy, cond_noise, 3), idx, ncl)
+    _check(_np(out), ref, f"cond split {policy} cond_noise={cond_noise}")
+
+
+@pytest.mark.parametrize("cond_noise", [False, True])
+def test_attention_kv_cache_matches_oracle(device, cond_noise):
+    """Cache the conditioning frames (return_kv), then continue the noise
+    frames from it (attention.py:235-275)."""
+    C, H, grid, ncl = 256, 2, (8, 8, 16), 4
+    N = int(np.prod(grid))
+    nc = N // grid[0] * ncl
+    noise_grid = (grid[0] - ncl,) + grid[1:]
+    blk = _block(C, H, 64, device, seed=9)
+    a = blk.attn
+    a.enable_bsa, a.bsa_chunk_thw, a.bsa_cond_noise, a.bsa_top_k, a.keep_indices = True, (4, 4, 4), cond_noise, 3, True
+    x, _, _ = _inputs(N, C, grid[0], 64, 8, device, seed=10)
+    with torch.no_grad():
+        _, (kc, vc) = a(x[:, :nc], (ncl,) + grid[1:], return_kv=True)
+        out = a.forward_with_kv_cache(x[:, nc:], noise_grid, ncl, (kc, vc))
+    assert a.last_paths["noise"] == ("bsa" if cond_noise else "dense")
+    bsa = _split_geoms(grid, ncl, (4, 4, 4), "reference", cond_noise, 3)
+    ref, _ = DB.self_attention_kv_cache(_np(x[:, nc:]), _attn_params(blk), noise_grid, H, "bf16",
+                                        (_np(kc), _np(vc)), ncl, bsa, _idx(blk))
+    _check(_np(out), ref, f"kv cache cond_noise={cond_noise}")
+
+
+def test_block_with_cond_latents_matches_oracle(device):
+    C, H, t_dim, L, grid, ncl = 256, 2, 64, 16, (8, 8, 16), 4
+    N = int(np.prod(grid))
+    blk = _block(C, H, t_dim, device, seed=11)
+    a = blk.attn
+    a.enable_bsa, a.bsa_chunk_thw, a.bsa_cond_noise, a.bsa_top_k, a.keep_indices = True, (4, 4, 4), True, 3, True
+    x, y, t = _inputs(N, C, grid[0], t_dim, L, device, seed=12)
+    with torch.no_grad():
+        out = blk(x, y, t, [L], grid, num_cond_latents=ncl)
+    p = {k: _np(v) for k, v in blk.state_dict().items()}
+    ref, _ = DB.dit_block(_np(x), _np(y), _np(t), p, grid, H, "bf16",
+                          _split_geoms(grid, ncl, (4, 4, 4), "reference", True, 3), _idx(blk), num_cond_latents=ncl)
+    _check(_np(out), ref, "block with cond latents")

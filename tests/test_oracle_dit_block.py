@@ -115,8 +115,9 @@ def test_self_attention_with_all_blocks_is_dense():
     p = _params(C, H)
     N = int(np.prod(grid))
     x = O.round_to(RNG.normal(size=(1, N, C)).astype(np.float32), "bf16")
-    bsa = dict(shape=(1, 1, N), chunk_thw=(1, 1, 64), top_k=N // 64)
+    bsa = {"all": ((1, 1, N), (1, 1, 64)), "top_k": N // 64}
     out, idx = DB.self_attention(x, p, grid, H, "bf16", bsa)
+    idx = idx["all"]
     assert np.array_equal(np.sort(idx, -1), np.broadcast_to(np.arange(N // 64), idx.shape))
     # Dense path through the oracle's own (pinned) pieces.
     D = C // H
@@ -165,7 +166,7 @@ def test_block_adaln_zero_identity_and_planted_gate():
     x = O.round_to(RNG.normal(size=(1, N, C)).astype(np.float32), "bf16")
     y = RNG.normal(size=(1, 5, C)).astype(np.float32)
     t = RNG.normal(size=(1, grid[0], 32)).astype(np.float32)
-    bsa = dict(shape=(1, 1, N), chunk_thw=(1, 1, 64), top_k=2)
+    bsa = {"all": ((1, 1, N), (1, 1, 64)), "top_k": 2}
     out, _ = DB.dit_block(x, y, t, p, grid, H, "bf16", bsa)
     assert np.array_equal(out, x)
     # A gate of one on the attention branch of frame 1 only changes frame 1's tokens.
@@ -178,3 +179,63 @@ def test_block_adaln_zero_identity_and_planted_gate():
     per = N // grid[0]
     assert np.array_equal(out2[:, :per], x[:, :per])
     assert not np.array_equal(out2[:, per:], x[:, per:])
+
+
+def _qkv_roped(x, p, grid, H, dtype="bf16"):
+    N, C = x.shape[1], x.shape[2]
+    D = C // H
+    qkv = DB.linear(x, p["attn.qkv.weight"], p["attn.qkv.bias"], dtype).reshape(1, N, 3, H, D)
+    q, k, v = (np.transpose(qkv[:, :, i], (0, 2, 1, 3)) for i in range(3))
+    q = O.rms_norm_fp32(q, p["attn.q_norm.weight"], 1e-6, dtype)
+    k = O.rms_norm_fp32(k, p["attn.k_norm.weight"], 1e-6, dtype)
+    f = O.rope_freqs_3d(grid, D).astype(np.float32)
+    return O.round_to(O.apply_rope(q, f), dtype), O.round_to(O.apply_rope(k, f), dtype), v
+
+
+def test_cond_split_with_all_blocks_is_masked_dense():
+    """attention.py:202-221 with every block selected: conditioning queries
+    see only conditioning keys, noise queries see all keys -- one dense
+    attention (torch's SDPA) under that mask."""
+    C, H, grid, ncl = 128, 2, (4, 8, 8), 2
+    N = int(np.prod(grid))
+    nc = N // grid[0] * ncl
+    p = _params(C, H, seed=3)
+    x = O.round_to(RNG.normal(size=(1, N, C)).astype(np.float32), "bf16")
+    bsa = {"cond": ((1, 1, nc), (1, 1, 64)), "noise": (((1, 1, N - nc), (1, 1, 64)), ((1, 1, N), (1, 1, 64))),
+           "top_k": 1}
+    every = {"cond": np.broadcast_to(np.arange(nc // 64), (1, H, nc // 64, nc // 64)),
+             "noise": np.broadcast_to(np.arange(N // 64), (1, H, (N - nc) // 64, N // 64))}
+    out_all, _ = DB.self_attention(x, p, grid, H, "bf16", bsa, block_indices=every, num_cond_latents=ncl)
+    q, k, v = _qkv_roped(x, p, grid, H)
+    mask = np.zeros((N, N))
+    mask[:nc, nc:] = -np.inf
+    o = torch.nn.functional.scaled_dot_product_attention(*(torch.from_numpy(a.astype(np.float64)) for a in (q, k, v)),
+                                                         attn_mask=torch.from_numpy(mask), scale=(C // H) ** -0.5)
+    o = O.round_to(o.numpy().astype(np.float32), "bf16")
+    ref = DB.linear(np.transpose(o, (0, 2, 1, 3)).reshape(1, N, C), p["attn.proj.weight"], p["attn.proj.bias"], "bf16")
+    assert np.allclose(out_all, ref, atol=2e-2, rtol=2e-2) and np.mean(out_all == ref) > 0.9
+    # The split is not the unsplit layer: conditioning rows differ from full attention.
+    full, _ = DB.self_attention(x, p, grid, H, "bf16", {"all": None, "top_k": 1})
+    assert not np.allclose(full[:, :nc], out_all[:, :nc], atol=1e-3)
+    assert np.allclose(full[:, nc:], out_all[:, nc:], atol=2e-2)
+
+
+def test_kv_cache_continuation_equals_split_noise_branch():
+    """attention.py:235-275: continuing from the cache of the conditioning
+    frames gives the noise rows of the conditioning split, when the chunk's
+    tokens are the noise frames (RoPE over the extended grid aligns them)."""
+    C, H, full_grid, ncl = 128, 2, (4, 8, 8), 2
+    N = int(np.prod(full_grid))
+    nc = N // full_grid[0] * ncl
+    p = _params(C, H, seed=4)
+    x = O.round_to(RNG.normal(size=(1, N, C)).astype(np.float32), "bf16")
+    dense = {"cond": None, "noise": None, "top_k": 1}
+    split, _ = DB.self_attention(x, p, full_grid, H, "bf16", dense, num_cond_latents=ncl)
+    # The cache: normed, un-rotated k / v of the conditioning frames.
+    D = C // H
+    qkv = DB.linear(x[:, :nc], p["attn.qkv.weight"], p["attn.qkv.bias"], "bf16").reshape(1, nc, 3, H, D)
+    kc = O.rms_norm_fp32(np.transpose(qkv[:, :, 1], (0, 2, 1, 3)), p["attn.k_norm.weight"], 1e-6, "bf16")
+    vc = np.transpose(qkv[:, :, 2], (0, 2, 1, 3))
+    noise_grid = (full_grid[0] - ncl,) + full_grid[1:]
+    cont, _ = DB.self_attention_kv_cache(x[:, nc:], p, noise_grid, H, "bf16", (kc, vc), ncl, dense)
+    assert np.array_equal(cont, split[:, nc:])
