@@ -378,6 +378,52 @@ def bench_kv_split(lib, dev, stream, steps: int, warmup: int, seed: int):
     }
 
 
+def bench_voxel_policy(lib, dev, stream, steps: int, warmup: int, seed: int):
+    """The block-geometry choice at a 720p-sized grid that the (4, 4, 4)
+    voxel can tile: (16, 48, 80) latents (720p padded from 45 to 48 rows),
+    B1 H32 D128 fp16, top-k 60 of 960 blocks.  The same q, k, v go through
+    the attention kernel once with (4, 4, 4) voxel blocks and once with
+    64-token runs, each with its own top-k routing."""
+    import torch
+
+    from lcv_bsa import _lib
+    from lcv_bsa.block_sparse_attention import _geom, _strides, mean_pool_blocks_3d, select_block_indices
+    from lcv_bsa.block_sparse_attention_hip import schedule_block_order
+    from lcv_bsa.workloads import make_inputs
+
+    grid, H, D, top_k = (16, 48, 80), 32, 128, 60
+    S = grid[0] * grid[1] * grid[2]
+    q, k, v, _ = make_inputs(1, H, D, grid, (4, 4, 4), torch.float16, dev, seed=seed + 5, grid=grid)
+    out = torch.empty_like(q)
+    sh = stream.cuda_stream
+    res = {}
+    for name, shape, chunk in (("voxel_4x4x4", grid, (4, 4, 4)), ("contiguous_64", (1, 1, S), (1, 1, 64))):
+        idx = select_block_indices(mean_pool_blocks_3d(q, shape, chunk), mean_pool_blocks_3d(k, shape, chunk), top_k)
+        order = schedule_block_order(idx)
+        geom = _geom(shape, chunk)
+
+        def attn():
+            _lib.check(lib.lcv_bsa_attn_fwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.F16, 1, H, S, D, _strides(q), _strides(k),
+                _strides(v), idx.data_ptr(), order.data_ptr(), top_k, 1.0 / math.sqrt(D), geom,
+                out.data_ptr(), _strides(out), sh), "attn")
+        for _ in range(warmup):
+            attn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            attn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        flop = 4 * H * (S // 64) * top_k * 64 * 64 * D
+        res[name] = {"ms_attention": round(ms, 4), "achieved": round(flop / (ms * 1e-3) / 1e12, 1)}
+    del q, k, v, out
+    torch.cuda.empty_cache()
+    return {"workload": "latents (16, 48, 80) = 61440 tokens, B1 H32 D128 fp16, top-k 60 of 960, same inputs", **res}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -553,6 +599,11 @@ def main() -> int:
         result["kv_split"] = kv
         log(f"S_q != S_k (continuation): attention {kv['ms_attention']:.3f} ms ({kv['achieved']:.0f} TFLOP/s, "
             f"{100 * kv['frac_of_2500']:.1f} %), pipeline {kv['ms_total']:.3f} ms; dense SDPA {kv['dense_sdpa_ms']} ms")
+    if args.config == "c2" and not args.no_kv_split:
+        vp = bench_voxel_policy(lib, dev, stream, args.steps, args.warmup, args.seed)
+        result["block_geometry"] = vp
+        log(f"geometry at (16,48,80): voxel {vp['voxel_4x4x4']['ms_attention']:.3f} ms, "
+            f"contiguous {vp['contiguous_64']['ms_attention']:.3f} ms")
     if args.config == "c2" and not args.no_dit_block:
         blk = bench_dit_block(dev, stream, max(3, args.steps // 2), 2, args.seed, top_k)
         result["dit_block"] = blk
