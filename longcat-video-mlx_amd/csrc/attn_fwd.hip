@@ -154,12 +154,19 @@ __device__ __forceinline__ void wait_vmcnt() {
 // lds_dst + 16 i (1 KB per wave).  Issued as inline asm so that the only
 // waits on it are the explicit wait_vmcnt<> calls (the compiler otherwise
 // waits for every outstanding LDS load before any LDS read).
+// The immediate OFF is added to both the memory and the LDS address, so four
+// loads 1 KB apart in LDS share one M0 value when each lane's voffset is
+// pre-reduced by OFF (the memory offset of a load's rows is at least OFF).
+template <int OFF>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, int32_t soffset,
-                                      const void* lds_dst) {
-  const uint32_t m0v = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
-               ::"v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(m0v)
+                                      uint32_t m0v) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen offset:%3 lds"
+               ::"v"(voffset), "s"(rsrc), "s"(soffset), "i"(OFF), "{m0}"(m0v)
                : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
 template <typename T>
@@ -274,23 +281,35 @@ void attn_mfma_kernel(AttnParams p) {
     const int row = t * C::kRowsPerDma + lane / C::DC;
     const int pos = lane % C::DC;
     const uint32_t tokoff = (uint32_t)voxel_row_offset(p.gk, row);
-    kvo[u] = (tokoff * (uint32_t)p.k_ss + 8u * (pos ^ C::kswz(row))) * sizeof(T);
-    vvo[u] = (tokoff * (uint32_t)p.v_ss + 8u * (pos ^ C::vswz(row))) * sizeof(T);
+    // Minus the load's immediate offset (1 KB x its place in a group of 4).
+    kvo[u] = (tokoff * (uint32_t)p.k_ss + 8u * (pos ^ C::kswz(row))) * sizeof(T) - 1024u * (u % 4);
+    vvo[u] = (tokoff * (uint32_t)p.v_ss + 8u * (pos ^ C::vswz(row))) * sizeof(T) - 1024u * (u % 4);
   }
+  static_assert(C::kDmaPerWave % 4 == 0, "DMA loads go in groups of four per M0 value");
   const uint32_t k_row_bytes = (uint32_t)p.k_ss * sizeof(T);
   const uint32_t v_row_bytes = (uint32_t)p.v_ss * sizeof(T);
   // tok: first token of the block (uniform).
   auto dma_k = [&](int32_t tok) {
     const int off = (int)((uint32_t)tok * k_row_bytes);
 #pragma unroll
-    for (int u = 0; u < C::kDmaPerWave; ++u)
-      dma16(krs, kvo[u], off, Ks + 1024 * (wave * C::kDmaPerWave + u));
+    for (int u = 0; u < C::kDmaPerWave; u += 4) {
+      const uint32_t m0v = lds_addr(Ks + 1024 * (wave * C::kDmaPerWave + u));
+      dma16<0>(krs, kvo[u], off, m0v);
+      dma16<1024>(krs, kvo[u + 1], off, m0v);
+      dma16<2048>(krs, kvo[u + 2], off, m0v);
+      dma16<3072>(krs, kvo[u + 3], off, m0v);
+    }
   };
   auto dma_v = [&](int32_t tok) {
     const int off = (int)((uint32_t)tok * v_row_bytes);
 #pragma unroll
-    for (int u = 0; u < C::kDmaPerWave; ++u)
-      dma16(vrs, vvo[u], off, Vs + 1024 * (wave * C::kDmaPerWave + u));
+    for (int u = 0; u < C::kDmaPerWave; u += 4) {
+      const uint32_t m0v = lds_addr(Vs + 1024 * (wave * C::kDmaPerWave + u));
+      dma16<0>(vrs, vvo[u], off, m0v);
+      dma16<1024>(vrs, vvo[u + 1], off, m0v);
+      dma16<2048>(vrs, vvo[u + 2], off, m0v);
+      dma16<3072>(vrs, vvo[u + 3], off, m0v);
+    }
   };
 
   // ---- Per-lane LDS read addresses (bytes).
@@ -326,9 +345,25 @@ void attn_mfma_kernel(AttnParams p) {
   const int slot = blockIdx.x / kNumXcd;
   const int n0 = (int)(((int64_t)(slot % kResident) * p.nk) / kResident);
   const int j0 = list.count_below(n0, p.gk);
+  // Lists of at most 64 entries sit in one chunk: walk them with a 64-bit
+  // mask of the valid entries not yet visited, rotated so that bit b is
+  // entry (b + j0) mod 64 (entries >= top_k are never valid).
+  const bool one_chunk = p.top_k <= 64;
+  const int r0 = j0 & 63;  // j0 may equal top_k = 64: a full turn
+  uint64_t rem = 0;
+  if (one_chunk) {
+    const uint64_t v = list.valid;
+    rem = r0 == 0 ? v : (v >> r0) | (v << (64 - r0));
+  }
   // Next valid position in rotated order after position j (j < 0: start);
   // returns top_k at the end.
   auto next_rot = [&](int j) -> int {
+    if (one_chunk) {
+      if (rem == 0) return p.top_k;
+      const int b = (int)__builtin_ctzll(rem);
+      rem &= rem - 1;
+      return (b + r0) & 63;
+    }
     if (j < 0 || j >= j0) {
       const int r = list.next(j < 0 ? j0 : j + 1, p.gk);
       if (r < p.top_k) return r;
