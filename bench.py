@@ -268,6 +268,8 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int)
     for h in handles:
         h.remove()
     per = {k: sum(a.elapsed_time(b) for a, b in v) / steps for k, v in marks.items()}
+    for k in mods:                     # sub-modules the fused path does not call
+        per.setdefault(k, 0.0)
     ms_instr = b0.elapsed_time(b1) / steps
     bsa_ms = per["self_attn"] - per["qkv_gemm"] - per["proj_gemm"]
     Hf = blk.ffn.hidden_dim
@@ -288,9 +290,10 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int)
             "self_attn_qkv_gemm": round(per["qkv_gemm"], 3),
             "self_attn_bsa (prepare_qk + routing + attention)": round(bsa_ms, 3),
             "self_attn_proj_gemm": round(per["proj_gemm"], 3),
-            "cross_attn (norm, 3 GEMMs, SDPA over 512 text tokens)": round(per["cross_attn"] + per["pre_cross_norm"], 3),
-            "ffn (3 GEMMs + SiLU gate)": round(ffn_ms, 3),
-            "adaln_modulation_and_residuals": round(other, 3),
+            "cross_attn (q/kv/proj GEMMs, q/k norms, attention over 512 text tokens)":
+                round(per["cross_attn"] + per["pre_cross_norm"], 3),
+            "ffn (w1|w3 and w2 GEMMs + SiLU gate)": round(ffn_ms, 3),
+            "adaln_modulation_residuals_and_pre_norm": round(other, 3),
         },
         "gemm_tflop": round(gemm_flop / 1e12, 3),
         "instrumented_ms": round(ms_instr, 3),

@@ -165,6 +165,49 @@ int lcv_bsa_attn_fwd_kv(const void* q, const void* k, const void* v, int dtype,
                         lcv_bsa_strides os, void* stream);
 
 /*
+ * DiT block row operation (one pass over [B, N, C] rows, fp16 / bf16):
+ *   r = x                      (a null)
+ *     = round(x + a)           (a given, gate null)
+ *     = round(x + gate * a)    (gate: fp32 [B, frames, C], per latent frame)
+ * written to x_out when given; then, when n_out is given,
+ *   y = LayerNorm_fp32(r; eps)  [* ln_weight + ln_bias]  [* (scale + 1) + shift]
+ * rounded to the dtype (shift / scale: fp32 [B, frames, C]).  N must be a
+ * multiple of frames (tokens of frame t: rows t*N/frames ..); C % 8 == 0,
+ * C <= 8192; every pointer 16-byte aligned, tensors contiguous.
+ * Replaces, in LongCatSingleStreamBlock.__call__ (longcat_video/models/
+ * longcat_video_dit.py:107-136): modulate_fp32 over LayerNorm_FP32
+ * (blocks.py:79-119), the fp32 gated residuals, the cross-attention residual
+ * and pre_crs_attn_norm -- each a chain of full-tensor passes there.
+ */
+int lcv_bsa_block_rows(const void* x, const void* a, int dtype, int64_t B,
+                       int64_t N, int64_t C, int64_t frames, const float* gate,
+                       const float* shift, const float* scale,
+                       const void* ln_weight, const void* ln_bias, float eps,
+                       void* x_out, void* n_out, void* stream);
+
+/*
+ * SwiGLU gate: out[r, j] = round(round(silu(h[r, j])) * h[r, hidden + j])
+ * for h = [rows, 2*hidden] (the w1 and w3 projections side by side) and
+ * out = [rows, hidden].  fp16 / bf16, hidden % 8 == 0, 16-byte aligned.
+ * Replaces silu(w1(x)) * w3(x) of FeedForwardSwiGLU (blocks.py:50-51).
+ */
+int lcv_bsa_block_swiglu(const void* h13, int dtype, int64_t rows,
+                         int64_t hidden, void* out, void* stream);
+
+/*
+ * Per-head RMSNorm_FP32 (blocks.py:55-72) of a [B,H,S,D] view into another
+ * [B,H,S,D] view (strides in elements, any layout with dense D):
+ *   out = round(round(x * rsqrt(mean(x^2) + eps)) * weight).
+ * weight: [D] in the dtype, or null for 1.  D in {64, 128}.  Used for the
+ * cross-attention's q_norm / k_norm (attention.py:325-326), reading the
+ * projection's [B, S, H, D] rows and writing the layout attention reads.
+ */
+int lcv_bsa_head_rms_norm(const void* x, int dtype, int64_t B, int64_t H,
+                          int64_t S, int64_t D, lcv_bsa_strides xs,
+                          const void* weight, float eps, void* out,
+                          lcv_bsa_strides os, void* stream);
+
+/*
  * Bytes of workspace lcv_bsa_forward needs: the fp32 pooled means of q and
  * k (2*B*H*nb*D*4 bytes) and the int32 launch order (B*H*nb*4 bytes), each
  * rounded up to 256 bytes.  Host only.

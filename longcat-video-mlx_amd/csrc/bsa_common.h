@@ -215,6 +215,18 @@ hipError_t launch_prep(const Tensor4* in, const Tensor4* out, const void* const*
                        const int32_t* rope_grid, const int32_t* rope_dims, const float* table,
                        int table_len, float eps, hipStream_t stream);
 
+// DiT block row operations (fp16 / bf16).
+bool rows_supported(int dtype, int C);
+hipError_t launch_rows(const void* x, const void* a, const float* gate, const float* shift,
+                       const float* scale, const void* ln_w, const void* ln_b, void* x_out,
+                       void* n_out, int dtype, int rows, int C, int rows_per_batch,
+                       int tokens_per_frame, int frames, float eps, hipStream_t stream);
+hipError_t launch_swiglu(const void* h, void* out, int dtype, int64_t rows, int hidden,
+                         hipStream_t stream);
+hipError_t launch_head_norm(const void* x, const int64_t* xs, void* out, const int64_t* os,
+                            const void* w, int dtype, int B, int N, int H, int D, float eps,
+                            hipStream_t stream);
+
 hipError_t launch_token_blocks(const Geom& g, int T, int32_t* out, hipStream_t stream);
 hipError_t launch_pair_mask(const int32_t* idx, int B, int H, int nq, int top_k,
                             const int32_t* token_block, int S, int nkv, uint8_t* mask,

@@ -347,6 +347,73 @@ int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype, int6
   return launch_status(lcv::launch_attn(p, dtype, (int)D, s), "lcv_bsa_forward(attn)");
 }
 
+int lcv_bsa_block_rows(const void* x, const void* a, int dtype, int64_t B, int64_t N, int64_t C,
+                       int64_t frames, const float* gate, const float* shift, const float* scale,
+                       const void* ln_weight, const void* ln_bias, float eps, void* x_out,
+                       void* n_out, void* stream) {
+  if (!x) return fail(LCV_BSA_ERR_INVALID_ARG, "null x");
+  if (dtype != LCV_BSA_F16 && dtype != LCV_BSA_BF16)
+    return fail(LCV_BSA_ERR_DTYPE, "block row ops take fp16 or bf16 (got dtype %d)", dtype);
+  if (B <= 0 || N <= 0 || C <= 0 || frames <= 0 || N % frames)
+    return fail(LCV_BSA_ERR_SHAPE, "B, N, C, frames must be positive with N %% frames == 0 "
+                "(B=%lld N=%lld C=%lld frames=%lld)", (long long)B, (long long)N, (long long)C,
+                (long long)frames);
+  if (!lcv::rows_supported(dtype, (int)C))
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "block row ops need C %% 8 == 0 and C <= 8192 (C=%lld)",
+                (long long)C);
+  if (B * N > kI32Max / 2 || B * N * C > (int64_t{1} << 40))
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "tensor too large");
+  if (gate && !a) return fail(LCV_BSA_ERR_INVALID_ARG, "gate needs a residual input a");
+  if (x_out && !a) return fail(LCV_BSA_ERR_INVALID_ARG, "x_out needs a residual input a");
+  if ((!shift) != (!scale)) return fail(LCV_BSA_ERR_INVALID_ARG, "shift and scale go together");
+  if ((!ln_weight) != (!ln_bias))
+    return fail(LCV_BSA_ERR_INVALID_ARG, "ln_weight and ln_bias go together");
+  if ((shift || ln_weight) && !n_out)
+    return fail(LCV_BSA_ERR_INVALID_ARG, "normalisation parameters given without n_out");
+  if (!x_out && !n_out) return fail(LCV_BSA_ERR_INVALID_ARG, "nothing to write");
+  const void* ptrs[] = {x, a, gate, shift, scale, ln_weight, ln_bias, x_out, n_out};
+  for (const void* q : ptrs)
+    if ((uintptr_t)q % 16) return fail(LCV_BSA_ERR_LAYOUT, "all tensors must be 16-byte aligned");
+  return launch_status(lcv::launch_rows(x, a, gate, shift, scale, ln_weight, ln_bias, x_out, n_out,
+                                        dtype, (int)(B * N), (int)C, (int)N, (int)(N / frames),
+                                        (int)frames, eps, (hipStream_t)stream),
+                       "lcv_bsa_block_rows");
+}
+
+int lcv_bsa_block_swiglu(const void* h13, int dtype, int64_t rows, int64_t hidden, void* out,
+                         void* stream) {
+  if (!h13 || !out) return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
+  if (dtype != LCV_BSA_F16 && dtype != LCV_BSA_BF16)
+    return fail(LCV_BSA_ERR_DTYPE, "swiglu takes fp16 or bf16 (got dtype %d)", dtype);
+  if (rows <= 0 || hidden <= 0 || hidden % 8 || rows * hidden > (int64_t{1} << 40) ||
+      hidden > kI32Max)
+    return fail(LCV_BSA_ERR_SHAPE, "swiglu needs rows > 0 and hidden a positive multiple of 8");
+  if ((uintptr_t)h13 % 16 || (uintptr_t)out % 16)
+    return fail(LCV_BSA_ERR_LAYOUT, "swiglu tensors must be 16-byte aligned");
+  return launch_status(lcv::launch_swiglu(h13, out, dtype, rows, (int)hidden, (hipStream_t)stream),
+                       "lcv_bsa_block_swiglu");
+}
+
+int lcv_bsa_head_rms_norm(const void* x, int dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                          lcv_bsa_strides xs, const void* weight, float eps, void* out,
+                          lcv_bsa_strides os, void* stream) {
+  if (!x || !out) return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
+  if (dtype != LCV_BSA_F16 && dtype != LCV_BSA_BF16)
+    return fail(LCV_BSA_ERR_DTYPE, "head RMSNorm takes fp16 or bf16 (got dtype %d)", dtype);
+  if (!(D == 64 || D == 128)) return fail(LCV_BSA_ERR_UNSUPPORTED, "head RMSNorm needs D in {64, 128}");
+  if (B <= 0 || H <= 0 || S <= 0 || B * H * S > kI32Max / 2)
+    return fail(LCV_BSA_ERR_SHAPE, "B, H, S must be positive and B*H*S < 2^30");
+  if (!std::isfinite(eps) || eps < 0.0f) return fail(LCV_BSA_ERR_INVALID_ARG, "eps must be >= 0");
+  int st = 0;
+  if ((st = check_strides("x", xs, D)) || (st = check_strides("out", os, D))) return st;
+  if (!vec_aligned(x, xs, 8) || !vec_aligned(out, os, 8) || (uintptr_t)weight % 16)
+    return fail(LCV_BSA_ERR_LAYOUT, "rows and weight must start on 16-byte boundaries");
+  const int64_t xst[3] = {xs.b, xs.s, xs.h}, ost[3] = {os.b, os.s, os.h};
+  return launch_status(lcv::launch_head_norm(x, xst, out, ost, weight, dtype, (int)B, (int)S,
+                                             (int)H, (int)D, eps, (hipStream_t)stream),
+                       "lcv_bsa_head_rms_norm");
+}
+
 int lcv_bsa_token_blocks(lcv_bsa_geom g, int32_t* out, void* stream) {
   if (!out) return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
   int64_t nb = 0, bs = 0;

@@ -64,6 +64,12 @@ _SIGNATURES = {
     "lcv_bsa_attn_fwd_kv": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
                                     c_int64, c_int64, Strides, Strides, Strides, c_void_p, c_void_p,
                                     c_int64, c_float, Geom, Geom, c_void_p, Strides, c_void_p]),
+    "lcv_bsa_block_rows": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64, c_int64,
+                                   c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float,
+                                   c_void_p, c_void_p, c_void_p]),
+    "lcv_bsa_block_swiglu": (c_int, [c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p]),
+    "lcv_bsa_head_rms_norm": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_int64, Strides,
+                                      c_void_p, c_float, c_void_p, Strides, c_void_p]),
     "lcv_bsa_forward_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int64]),
     "lcv_bsa_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
                                 c_int64, Strides, Strides, Strides, c_int64, c_float, Geom,

@@ -24,7 +24,9 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .attention import BSAAttention, dense_attention, validate_backend
+from .block_ops import head_rms_norm, residual_norm, swiglu
 from .block_sparse_attention import bsa_attention
+from .block_sparse_attention_hip import bsa_attention_hip
 from .prepare import prepare_qk
 from .rope_3d import rope_3d
 from .shape_policy import bsa_geometry
@@ -89,7 +91,21 @@ class FeedForwardSwiGLU(nn.Module):
         self.w2 = nn.Linear(hidden_dim, dim, bias=False, **kw)
         self.w3 = nn.Linear(dim, hidden_dim, bias=False, **kw)
 
+        self.fused = True            # on the GPU: one w1|w3 GEMM + the HIP gate kernel
+        self._w13 = None
+        self._w13_key = None
+
+    def _w13_weight(self) -> torch.Tensor:
+        key = (self.w1.weight.data_ptr(), self.w1.weight._version, self.w3.weight.data_ptr(),
+               self.w3.weight._version)
+        if self._w13_key != key:
+            self._w13 = torch.cat([self.w1.weight, self.w3.weight], 0).detach()
+            self._w13_key = key
+        return self._w13
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.fused and x.is_cuda and self.hidden_dim % 8 == 0:
+            return self.w2(swiglu(F.linear(x, self._w13_weight())))
         return self.w2(F.silu(self.w1(x)) * self.w3(x))
 
 
@@ -248,6 +264,9 @@ class MultiHeadCrossAttention(nn.Module):
         self.proj = nn.Linear(dim, dim, **kw)
         self.q_norm = RMSNorm_FP32(self.head_dim, eps=1e-6, **kw)
         self.k_norm = RMSNorm_FP32(self.head_dim, eps=1e-6, **kw)
+        # On the GPU, with 64-aligned token and text lengths: fused norms and
+        # the library's attention kernel (dense over the text blocks).
+        self.fused = True
 
     def forward(self, x: torch.Tensor, cond: torch.Tensor, kv_seqlen: Sequence[int],
                 num_cond_latents: Optional[int] = None, shape: Optional[Sequence[int]] = None) -> torch.Tensor:
@@ -261,9 +280,35 @@ class MultiHeadCrossAttention(nn.Module):
             return torch.cat([out_noise.new_zeros((B, nc, C)), out_noise], dim=1)
         return self._cross(x, cond, kv_seqlen)
 
+    def _cross_fused(self, x, cond, kv_seqlen):
+        """q / k norms in place on the projections' rows, then the library's
+        attention kernel with every text block listed (dense over the text),
+        written in the [B, N, H, D] layout the projection reads."""
+        B, N, C = x.shape
+        H, D = self.num_heads, self.head_dim
+        q = self.q_linear(x).view(B, N, H, D).transpose(1, 2)      # [B, H, N, D] view
+        head_rms_norm(q, self.q_norm.weight, self.q_norm.eps, out=q)
+        kv = self.kv_linear(cond).view(1, -1, 2, H, D)
+        k = kv[:, :, 0].transpose(1, 2)
+        head_rms_norm(k, self.k_norm.weight, self.k_norm.eps, out=k)
+        v = kv[:, :, 1].transpose(1, 2)
+        o = torch.empty((B, N, H, D), dtype=x.dtype, device=x.device)
+        off = 0
+        for b in range(B):
+            n = int(kv_seqlen[b])
+            nk = n // 64
+            idx = torch.arange(nk, dtype=torch.int32, device=x.device).expand(1, H, N // 64, nk).contiguous()
+            bsa_attention_hip(q[b:b + 1], k[:, :, off:off + n], v[:, :, off:off + n], idx, (1, 1, 64),
+                              (1, 1, N), self.scale, out=o[b:b + 1].transpose(1, 2), kv_shape=(1, 1, n))
+            off += n
+        return self.proj(o.view(B, N, C))
+
     def _cross(self, x: torch.Tensor, cond: torch.Tensor, kv_seqlen: Sequence[int]) -> torch.Tensor:
         B, N, C = x.shape
         H, D = self.num_heads, self.head_dim
+        if (self.fused and x.is_cuda and N % 64 == 0 and all(int(n) % 64 == 0 for n in kv_seqlen)
+                and D in (64, 128) and x.dtype in (torch.float16, torch.bfloat16)):
+            return self._cross_fused(x, cond, kv_seqlen)
         q = self.q_norm(self.q_linear(x).view(B, N, H, D)).transpose(1, 2).contiguous()
         kv = self.kv_linear(cond).view(1, -1, 2, H, D)
         k = self.k_norm(kv[:, :, 0]).transpose(1, 2).contiguous()
@@ -291,6 +336,34 @@ class LongCatSingleStreamBlock(nn.Module):
         self.attn = Attention(hidden_size, num_heads, **kw)
         self.cross_attn = MultiHeadCrossAttention(hidden_size, num_heads, **kw)
         self.ffn = FeedForwardSwiGLU(hidden_size, int(hidden_size * mlp_ratio), **kw)
+        # On the GPU: modulation, gated residuals and the pre-norm as fused
+        # HIP row passes (same fp32 arithmetic as the unfused path below).
+        self.fused = True
+
+    def _self_attn(self, x_m, latent_shape, num_cond_latents, return_kv, kv_cache):
+        if kv_cache is not None:
+            return self.attn.forward_with_kv_cache(x_m, latent_shape, num_cond_latents, kv_cache), kv_cache
+        if return_kv:
+            return self.attn(x_m, latent_shape, num_cond_latents, return_kv=True)
+        return self.attn(x_m, latent_shape, num_cond_latents), None
+
+    def _forward_fused(self, x, y, t, y_seqlen, latent_shape, num_cond_latents, return_kv, kv_cache,
+                       skip_crs_attn, ada):
+        T = int(latent_shape[0])
+        shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = ada.chunk(6, dim=-1)
+        _, x_m = residual_norm(x, frames=T, shift=shift_msa, scale=scale_msa, eps=self.mod_norm_attn.eps)
+        x_s, new_kv = self._self_attn(x_m, latent_shape, num_cond_latents, return_kv, kv_cache)
+        pre = self.pre_crs_attn_norm
+        x, xn = residual_norm(x, x_s, gate_msa, frames=T, weight=pre.weight, bias=pre.bias, eps=pre.eps,
+                              norm=not skip_crs_attn)
+        if not skip_crs_attn:
+            ncl_cross = None if kv_cache is not None else num_cond_latents
+            c = self.cross_attn(xn, y, y_seqlen, ncl_cross, latent_shape)
+            x, x_m = residual_norm(x, c, frames=T, shift=shift_mlp, scale=scale_mlp, eps=self.mod_norm_ffn.eps)
+        else:
+            _, x_m = residual_norm(x, frames=T, shift=shift_mlp, scale=scale_mlp, eps=self.mod_norm_ffn.eps)
+        x, _ = residual_norm(x, self.ffn(x_m), gate_mlp, frames=T, norm=False)
+        return (x, new_kv) if return_kv else x
 
     def forward(self, x: torch.Tensor, y: torch.Tensor, t: torch.Tensor, y_seqlen: Sequence[int],
                 latent_shape: Sequence[int], num_cond_latents: Optional[int] = None, return_kv: bool = False,
@@ -305,15 +378,11 @@ class LongCatSingleStreamBlock(nn.Module):
         ada = F.linear(F.silu(t.float()), lin.weight.float(), lin.bias.float())[:, :, None, :]
         shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = ada.chunk(6, dim=-1)
 
+        if self.fused and x.is_cuda and x.dtype in (torch.float16, torch.bfloat16) and C % 8 == 0:
+            return self._forward_fused(x, y, t, y_seqlen, latent_shape, num_cond_latents, return_kv, kv_cache,
+                                       skip_crs_attn, ada)
         x_m = modulate_fp32(self.mod_norm_attn, x.view(B, T, -1, C), shift_msa, scale_msa).view(B, N, C)
-        new_kv = None
-        if kv_cache is not None:
-            x_s = self.attn.forward_with_kv_cache(x_m, latent_shape, num_cond_latents, kv_cache)
-            new_kv = kv_cache
-        elif return_kv:
-            x_s, new_kv = self.attn(x_m, latent_shape, num_cond_latents, return_kv=True)
-        else:
-            x_s = self.attn(x_m, latent_shape, num_cond_latents)
+        x_s, new_kv = self._self_attn(x_m, latent_shape, num_cond_latents, return_kv, kv_cache)
         x = (x.float() + (gate_msa * x_s.view(B, T, -1, C).float()).view(B, N, C)).to(dtype)
 
         if not skip_crs_attn:
