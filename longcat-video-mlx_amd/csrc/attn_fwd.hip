@@ -103,18 +103,27 @@ __device__ __forceinline__ int next_valid(const int32_t* list, int j, int top_k,
 struct TileList {
   const int32_t* list;
   int top_k, nb, base;
+  int raw;         // per lane: list entry base + l (INT_MAX past top_k)
   int tok;         // per lane
   uint64_t valid;  // bit l: entry base + l is a block in [0, nb)
-  __device__ TileList(const int32_t* l, int k, int n, const Geom& g) : list(l), top_k(k), nb(n) {
-    load(0, g);
+  // Issues the load of entries 0..63; finish() converts them once they are
+  // needed, so other loads can be in flight meanwhile.
+  __device__ TileList(const int32_t* l, int k, int n) : list(l), top_k(k), nb(n), base(0) {
+    raw = fetch(0);
+  }
+  __device__ int fetch(int b) const {
+    const int j = b + lane_id();
+    return j < top_k ? list[j] : 0x7fffffff;
+  }
+  __device__ void finish(const Geom& g) {
+    const bool ok = raw >= 0 && raw < nb;
+    tok = ok ? block_base_token(g, raw) : -1;
+    valid = __ballot(ok);
   }
   __device__ void load(int b, const Geom& g) {
     base = b;
-    const int j = b + lane_id();
-    const int n = j < top_k ? list[j] : -1;
-    const bool ok = n >= 0 && n < nb;
-    tok = ok ? block_base_token(g, n) : -1;
-    valid = __ballot(ok);
+    raw = fetch(b);
+    finish(g);
   }
   // First j' >= j whose entry is valid, or top_k.  j uniform.
   __device__ int next(int j, const Geom& g) {
@@ -130,13 +139,13 @@ struct TileList {
   __device__ int32_t token(int j) const { return __builtin_amdgcn_readlane(tok, j - base); }
   // Number of entries before the first one >= n0 in an ascending list (for
   // any list: the count of leading entries < n0, which is a valid start).
+  // Called with the first chunk in place; a one-chunk list needs no load.
   __device__ int count_below(int n0, const Geom& g) {
-    int cnt = 0;
-    for (int b = 0; b < top_k; b += 64) {
-      if (b != base) load(b, g);
-      const int j = b + lane_id();
-      const int n = j < top_k ? list[j] : 0x7fffffff;
-      const int c = __popcll(__ballot(n < n0));
+    int cnt = __popcll(__ballot(raw < n0));
+    if (cnt < 64 || top_k <= 64) return cnt;
+    for (int b = 64; b < top_k; b += 64) {
+      load(b, g);
+      const int c = __popcll(__ballot(raw < n0));
       cnt += c;
       if (c < 64) break;
     }
@@ -256,6 +265,11 @@ void attn_mfma_kernel(AttnParams p) {
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, (int)p.v_head_bytes, kBufferFlags);
 
+  // The routing list's load goes out first, the Q loads behind it: the list
+  // is needed first (it names the first tile), the Q fragments only at the
+  // first QK^T.
+  TileList list(p.idx + ((int64_t)bh * p.nb + qb) * p.top_k, p.top_k, p.nk);
+
   // ---- Q tile: B operand of S^T = K Q^T; lane holds Q[row][16ks + 8g .. +8].
   const int32_t qtok = block_base_token(p.g, qb) + voxel_row_offset(p.g, 32 * wave + l32);
   vec8 qf[D / 16];
@@ -264,12 +278,8 @@ void attn_mfma_kernel(AttnParams p) {
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks)
       qf[ks] = __builtin_bit_cast(vec8, *reinterpret_cast<const u32x4*>(qrow + 16 * ks));
-    // Consume the fragments here so the compiler's own vmcnt bookkeeping
-    // retires these loads before the tile loop; inside the loop the only
-    // outstanding vector loads are the tile DMAs, waited on explicitly.
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) asm volatile("" ::"v"(qf[ks]));
   }
+  list.finish(p.gk);
 
   // ---- Direct-to-LDS loads: wave load t fills LDS bytes [1024 t, 1024 t + 1024)
   // = rows t*RPD .. +RPD; lane i writes chunk position i % DC of row
@@ -334,7 +344,6 @@ void attn_mfma_kernel(AttnParams p) {
   bool first = true;   // wave-uniform
   const float sl2 = p.scale_log2;   // >= 0 on this path
 
-  TileList list(p.idx + ((int64_t)bh * p.nb + qb) * p.top_k, p.top_k, p.nk, p.gk);
   // Tile order: the list rotated to start at the first entry >= n0, where
   // n0 follows this workgroup's launch slot across [0, nk).  Workgroups that
   // are resident together start near the same block index and then advance
@@ -378,6 +387,12 @@ void attn_mfma_kernel(AttnParams p) {
     dma_k(tok);
     dma_v(tok);
   }
+  // Consume the Q fragments here, behind the first tile's DMAs, so the
+  // compiler's own vmcnt bookkeeping retires these loads before the tile
+  // loop; inside the loop the only outstanding vector loads are the tile
+  // DMAs, waited on explicitly.
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) asm volatile("" ::"v"(qf[ks]));
   while (j < p.top_k) {
     const int jn = next_rot(j);
     const int32_t njn = jn < p.top_k ? list.token(jn) : 0;

@@ -17,13 +17,16 @@ namespace {
 
 constexpr int kWavesPerWg = 4;
 
+// Raw 16-byte (or one-element) loads and their accumulation, split so that
+// several rows' loads can be in flight before any of them is added.
 template <typename T, int VEC>
 struct VecLoad;
 
 template <typename T>
 struct VecLoad<T, 8> {  // 8 x 16-bit
-  __device__ static void load(const T* p, float* acc) {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+  typedef u32x4 Raw;
+  __device__ static Raw load(const T* p) { return *reinterpret_cast<const u32x4*>(p); }
+  __device__ static void add(const Raw& w, float* acc) {
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       acc[2 * m] += to_f32(__builtin_bit_cast(T, (uint16_t)(w[m] & 0xffffu)));
@@ -34,8 +37,9 @@ struct VecLoad<T, 8> {  // 8 x 16-bit
 
 template <>
 struct VecLoad<float, 4> {
-  __device__ static void load(const float* p, float* acc) {
-    const f32x4 w = *reinterpret_cast<const f32x4*>(p);
+  typedef f32x4 Raw;
+  __device__ static Raw load(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+  __device__ static void add(const Raw& w, float* acc) {
 #pragma unroll
     for (int m = 0; m < 4; ++m) acc[m] += w[m];
   }
@@ -43,8 +47,13 @@ struct VecLoad<float, 4> {
 
 template <typename T>
 struct VecLoad<T, 1> {
-  __device__ static void load(const T* p, float* acc) { acc[0] += to_f32(*p); }
+  typedef T Raw;
+  __device__ static Raw load(const T* p) { return *p; }
+  __device__ static void add(const Raw& w, float* acc) { acc[0] += to_f32(w); }
 };
+
+constexpr int kRowTable = 256;  // voxel rows whose offsets are tabulated in LDS
+constexpr int kBatch = 8;       // row loads in flight per lane
 
 struct PoolArgs {
   Tensor4 x[2];
@@ -58,6 +67,13 @@ struct PoolArgs {
 template <typename T, int VEC>
 __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
   __shared__ float part[kWavesPerWg][64 * VEC];
+  __shared__ int32_t row_off[kRowTable];
+  // Token offset of each voxel row from the block's first token: the same
+  // for every block, so computed once per workgroup.
+  const bool table = a.bs <= kRowTable;
+  if (table)
+    for (int r = threadIdx.x; r < a.bs; r += blockDim.x) row_off[r] = voxel_row_offset(a.g, r);
+  __syncthreads();
   const int wave = threadIdx.x / 64;
   const int lane = threadIdx.x % 64;
   const int item_raw = blockIdx.x * kWavesPerWg + wave;
@@ -88,10 +104,25 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
     if (valid && p < P) {
-      for (int r = p; r < a.bs; r += P) {
-        const int32_t s = tok0 + voxel_row_offset(a.g, r);
-        VecLoad<T, VEC>::load(base + (int64_t)s * x.ss + c * VEC, acc);
+      typedef VecLoad<T, VEC> L;
+      const T* col = base + c * VEC;
+      // Rows p, p + P, p + 2P, ... are added in this order either way; the
+      // batches only put kBatch loads in flight before the adds.
+      int r = p;
+      if (table) {
+        for (; r + (kBatch - 1) * P < a.bs; r += kBatch * P) {
+          typename L::Raw w[kBatch];
+#pragma unroll
+          for (int u = 0; u < kBatch; ++u)
+            w[u] = L::load(col + (int64_t)(tok0 + row_off[r + u * P]) * x.ss);
+          // Keep the scheduler from pairing each load with its add.
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int u = 0; u < kBatch; ++u) L::add(w[u], acc);
+        }
       }
+      for (; r < a.bs; r += P)
+        L::add(L::load(col + (int64_t)(tok0 + voxel_row_offset(a.g, r)) * x.ss), acc);
     }
     // Combine the P partial sums of each column chunk in phase order.
 #pragma unroll

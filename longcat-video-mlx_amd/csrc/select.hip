@@ -190,9 +190,11 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
 // Score rows on fp32 MFMA (v_mfma_f32_16x16x4_f32).  One workgroup = 16
 // q-block rows of one (b, h); wave w computes the 16-column score tiles
 // w, w + 4, ... .  Operands come straight from global memory into registers:
-// lane (c, kg) (c = lane % 16, kg = lane / 16) holds dims [kg*D/4, (kg+1)*D/4)
-// of q-block row c (A) and of key row 16t + c (B), so k-step s pairs dim
-// kg*D/4 + s of both.  The accumulator holds S[4kg + i][16t + c].  kSelect
+// k-step s = 4 s4 + u of lane (c, kg) (c = lane % 16, kg = lane / 16) pairs
+// dim 16 s4 + 4 kg + u of q-block row c (A) and of key row 16t + c (B), so
+// the four kg lanes of a row load 64 contiguous bytes per instruction (16
+// cache lines per wave load, not 64).  The accumulator holds
+// S[4kg + i][16t + c].  kSelect
 // gathers the 16 x nk rows in LDS and runs wave_topk on them; kScoresOnly
 // writes the tiles to global memory.
 template <int NPER, int MODE, int D>
@@ -218,7 +220,7 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(RouteArgs a) {
 #pragma unroll
     for (int s4 = 0; s4 < DQ / 4; ++s4) {
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      if (row < a.nq) v = *reinterpret_cast<const f32x4*>(qb + (int64_t)row * D + kg * DQ + 4 * s4);
+      if (row < a.nq) v = *reinterpret_cast<const f32x4*>(qb + (int64_t)row * D + 16 * s4 + 4 * kg);
 #pragma unroll
       for (int u = 0; u < 4; ++u) qa[4 * s4 + u] = v[u];
     }
@@ -229,7 +231,7 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(RouteArgs a) {
 #pragma unroll
     for (int s4 = 0; s4 < DQ / 4; ++s4) {
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      if (key < a.nk) v = *reinterpret_cast<const f32x4*>(kb + (int64_t)key * D + kg * DQ + 4 * s4);
+      if (key < a.nk) v = *reinterpret_cast<const f32x4*>(kb + (int64_t)key * D + 16 * s4 + 4 * kg);
 #pragma unroll
       for (int u = 0; u < 4; ++u) kv[4 * s4 + u] = v[u];
     }
