@@ -491,10 +491,13 @@ def main() -> int:
     ws_bytes = lib.lcv_bsa_forward_workspace_bytes(B, H, nb, D)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     assert ws.data_ptr() % 256 == 0
-    pooled = (B * H * nb * D * 4 + 255) // 256 * 256  # workspace layout: qbar, kbar, order
+    # Workspace layout: qbar, kbar, block scores, launch order (256-byte aligned).
+    pooled = (B * H * nb * D * 4 + 255) // 256 * 256
+    scored = (B * H * nb * nb * 4 + 255) // 256 * 256
     qbar = ws[:pooled].view(torch.float32)
     kbar = ws[pooled:2 * pooled].view(torch.float32)
-    order = ws[2 * pooled:2 * pooled + B * H * nb * 4].view(torch.int32)
+    score = ws[2 * pooled:2 * pooled + B * H * nb * nb * 4].view(torch.float32)
+    order = ws[2 * pooled + scored:2 * pooled + scored + B * H * nb * 4].view(torch.int32)
     geom = _geom(w.shape, w.chunk_thw)
     qs, ks, vs, os_ = _strides(w.q), _strides(w.k), _strides(w.v), _strides(out)
     stream = torch.cuda.current_stream(dev)
@@ -511,8 +514,10 @@ def main() -> int:
         _lib.check(lib.lcv_bsa_pool(w.k.data_ptr(), code, B, H, S, D, ks, geom, kbar.data_ptr(), sh), "pool k")
 
     def stage_select():
-        _lib.check(lib.lcv_bsa_select(qbar.data_ptr(), kbar.data_ptr(), B, H, nb, nb, D, top_k,
-                                      idx.data_ptr(), sh), "select")
+        _lib.check(lib.lcv_bsa_scores(qbar.data_ptr(), kbar.data_ptr(), B, H, nb, nb, D,
+                                      score.data_ptr(), sh), "scores")
+        _lib.check(lib.lcv_bsa_topk(score.data_ptr(), B, H, nb, nb, top_k, idx.data_ptr(), sh),
+                   "top-k")
         _lib.check(lib.lcv_bsa_schedule(idx.data_ptr(), B, H, nb, top_k, order.data_ptr(), sh),
                    "schedule")
 

@@ -209,8 +209,9 @@ int lcv_bsa_head_rms_norm(const void* x, int dtype, int64_t B, int64_t H,
 
 /*
  * Bytes of workspace lcv_bsa_forward needs: the fp32 pooled means of q and
- * k (2*B*H*nb*D*4 bytes) and the int32 launch order (B*H*nb*4 bytes), each
- * rounded up to 256 bytes.  Host only.
+ * k (2*B*H*nb*D*4 bytes), the fp32 block scores (B*H*nb*nb*4 bytes) and the
+ * int32 launch order (B*H*nb*4 bytes), each rounded up to 256 bytes.  Host
+ * only.
  */
 size_t lcv_bsa_forward_workspace_bytes(int64_t B, int64_t H, int64_t nb,
                                        int64_t D);

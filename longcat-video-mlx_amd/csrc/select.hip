@@ -12,7 +12,8 @@
 // never writes scores to memory.
 //
 // Top-k is an exact radix select on order-preserving 32-bit keys: a 32-step
-// binary search finds the k-th largest key with ballot/popcount counts, then
+// binary search finds the k-th largest key with ballot/popcount counts (over
+// the keys above a cheap exact lower bound, compacted, when k <= 128), then
 // one ordered pass emits the indices of keys above it plus the lowest-index
 // keys equal to it, in ascending index order.  Equal scores therefore resolve
 // to the lower block index; NaN ranks below -inf; -0.0 equals +0.0.
@@ -32,10 +33,58 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+constexpr int kCompactCap = 512;  // compacted keys per wave (LDS words)
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t y = (uint32_t)__shfl_xor((int)x, o);
+    x = y < x ? y : x;
+  }
+  return x;
+}
+
+// Largest t with #(key >= t) >= k, built bit by bit over R keys per lane
+// (padding keys are 0 and never reach a candidate >= 1).  Once a candidate
+// at or above `floor` has exactly k keys at or above it, those keys are the
+// top k and the remaining bits cannot change the selection.
+template <int R>
+__device__ uint32_t kth_key(const uint32_t (&key)[R], int k, uint32_t floor) {
+  uint32_t thr = 0u;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = thr | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) cnt += __popcll(ballot64(key[r] >= cand));
+    if (cnt >= k) {
+      thr = cand;
+      if (cnt == k && cand >= floor) break;
+    }
+  }
+  return thr;
+}
+
+template <int R>
+__device__ uint32_t kth_key_compacted(const uint32_t* buf, int total, int k, uint32_t floor) {
+  const int lane = lane_id();
+  uint32_t key[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) key[r] = lane + 64 * r < total ? buf[lane + 64 * r] : 0u;
+  return kth_key<R>(key, k, floor);
+}
+
 // Exact top-k of one score row held as sc[e] = score[e*64 + lane], e < NPER.
-// Writes the k selected column indices, ascending, to out[0..k).
+// Writes the k selected column indices, ascending, to out[0..k).  buf:
+// kCompactCap words of this wave's LDS.
+//
+// For k <= 64 (and nk >= 64) a lower bound on the k-th largest key comes
+// first: every lane's largest key is >= L = their minimum, so at least
+// 64 >= k keys are >= L and the k-th largest key is among the keys >= L.
+// Those (typically a quarter of the row) are compacted into 4 or 8
+// registers per lane and searched there; counts at candidates >= L equal
+// the full row's, below L both are >= k, so the threshold is the full row's.
 template <int NPER>
-__device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out) {
+__device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out, uint32_t* buf) {
   const int lane = lane_id();
   uint32_t key[NPER];
 #pragma unroll
@@ -43,25 +92,36 @@ __device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out) 
     const int col = e * 64 + lane;
     key[e] = col < nk ? order_key(sc[e]) : 0u;
   }
-  // Largest threshold t with #(key >= t) >= k, built bit by bit.  Padding
-  // columns carry key 0 and never reach a candidate >= 1.  Once a candidate
-  // has exactly k keys at or above it, those keys are the top k and the
-  // remaining bits cannot change the selection.
   uint32_t thr = 0u;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = thr | (1u << bit);
-    int cnt = 0;
+  bool found = false;
+  if (k <= 64 && nk >= 64) {  // wave-uniform
+    uint32_t lane_max = 0u;
 #pragma unroll
-    for (int e = 0; e < NPER; ++e) cnt += __popcll(ballot64(key[e] >= cand));
-    if (cnt >= k) {
-      thr = cand;
-      if (cnt == k) break;
+    for (int e = 0; e < NPER; ++e) lane_max = key[e] > lane_max ? key[e] : lane_max;
+    const uint32_t L = wave_min_u32(lane_max);
+    int total = 0;
+#pragma unroll
+    for (int e = 0; e < NPER; ++e) {
+      const bool in = e * 64 + lane < nk && key[e] >= L;
+      const uint64_t msk = ballot64(in);
+      const int pos = total + (int)mbcnt64(msk);
+      if (in && pos < kCompactCap) buf[pos] = key[e];
+      total += __popcll(msk);
+    }
+    if (total <= 256) {
+      thr = kth_key_compacted<4>(buf, total, k, L);
+      found = true;
+    } else if (total <= kCompactCap) {
+      thr = kth_key_compacted<8>(buf, total, k, L);
+      found = true;
     }
   }
+  if (!found) thr = kth_key<NPER>(key, k, 0u);
+
   int gt = 0;
 #pragma unroll
   for (int e = 0; e < NPER; ++e) gt += __popcll(ballot64(key[e] > thr));
-  const int need_eq = k - gt;  // >= 1
+  const int need_eq = k - gt;
   int run_sel = 0, run_eq = 0;
 #pragma unroll
   for (int e = 0; e < NPER; ++e) {
@@ -87,6 +147,7 @@ struct RouteArgs {
   int32_t* idx;
   int32_t H, nq, nk, D, top_k;
   int32_t tiles_per_bh;
+  int32_t col_splits;
 };
 
 enum RouteMode { kSelect = 0, kScoresOnly = 1, kTopkOnly = 2 };
@@ -99,6 +160,7 @@ template <int NPER, int RW, int MODE>
 __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   __shared__ __attribute__((aligned(16))) float kch[kKeyChunk * (kMaxD + 4)];
   __shared__ __attribute__((aligned(16))) float qt[4 * RW * kMaxD];
+  __shared__ uint32_t tk_buf[4][kCompactCap];
   const int tid = threadIdx.x;
   const int wave = tid / 64;
   const int lane = tid % 64;
@@ -182,7 +244,8 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
     for (int r = 0; r < RW; ++r) {
       const int row = row0 + r;
       if (row >= a.nq) continue;  // wave-uniform
-      wave_topk<NPER>(sc[r], a.nk, a.top_k, a.idx + ((int64_t)bh * a.nq + row) * a.top_k);
+      wave_topk<NPER>(sc[r], a.nk, a.top_k, a.idx + ((int64_t)bh * a.nq + row) * a.top_k,
+                      tk_buf[wave]);
     }
   }
 }
@@ -204,6 +267,7 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(RouteArgs a) {
   constexpr int LDSW = NPER * 64 + 4;       // score row stride (floats)
   constexpr int kLds = MODE == kSelect ? QR * LDSW : 1;
   __shared__ __attribute__((aligned(16))) float srow[kLds];
+  __shared__ uint32_t tk_buf[MODE == kSelect ? 4 : 1][MODE == kSelect ? kCompactCap : 1];
   const int tid = threadIdx.x;
   const int wave = tid / 64;
   const int lane = tid % 64;
@@ -273,14 +337,128 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(RouteArgs a) {
       float sc[NPER];
 #pragma unroll
       for (int e = 0; e < NPER; ++e) sc[e] = srow[r * LDSW + e * 64 + lane];
-      wave_topk<NPER>(sc, a.nk, a.top_k, a.idx + ((int64_t)bh * a.nq + row) * a.top_k);
+      wave_topk<NPER>(sc, a.nk, a.top_k, a.idx + ((int64_t)bh * a.nq + row) * a.top_k,
+                      tk_buf[wave]);
     }
   }
 }
 
+// Score matrix S = qbar kbar^T on fp32 MFMA (v_mfma_f32_16x16x4_f32), written
+// to memory.  One workgroup = 4 waves x 16 q-block rows (64 rows) of one
+// (b, h) over a range of 64-key chunks (col_splits ranges per row tile, so
+// that small heads still fill the GPU).  A chunk's kbar rows are staged in
+// LDS (row stride D + 4 floats: the 16-byte operand reads are conflict free)
+// from coalesced 16-byte loads, which for the next chunk are in flight while
+// the current chunk's MFMAs run.  Each wave keeps its rows' qbar in
+// registers and runs the chunk's four 16-key tiles as four interleaved MFMA
+// chains.  k-step s = 4 s4 + u of lane (c, kg) pairs dim 16 s4 + 4 kg + u of
+// q-block row c and of key row 16t + c; the accumulator holds
+// S[4kg + i][16t + c].
+template <int D>
+__global__ __launch_bounds__(256) void scores_kernel(RouteArgs a) {
+  constexpr int KC = 64;              // keys per chunk
+  constexpr int KS = D + 4;           // LDS row stride (floats)
+  constexpr int DQ = D / 4;           // k-steps per tile
+  constexpr int D4 = D / 4;           // 16-byte pieces per row
+  constexpr int kLoads = KC * D4 / 256;
+  static_assert(kLoads * 256 == KC * D4, "chunk loads split evenly over the workgroup");
+  __shared__ __attribute__((aligned(16))) float kch[KC * KS];
+  const int tid = threadIdx.x;
+  const int wave = tid / 64;
+  const int lane = tid % 64;
+  const int c = lane % 16;
+  const int kg = lane / 16;
+  const int per_bh = a.tiles_per_bh * a.col_splits;
+  const int bh = blockIdx.x / per_bh;
+  const int rem = blockIdx.x - bh * per_bh;
+  const int rt = rem / a.col_splits;
+  const int cs = rem - rt * a.col_splits;
+  const int row0 = rt * 64 + wave * 16;
+  const int nchunks = (a.nk + KC - 1) / KC;
+  const int ch0 = (int)((int64_t)cs * nchunks / a.col_splits);
+  const int ch1 = (int)((int64_t)(cs + 1) * nchunks / a.col_splits);
+  const float* qb = a.qbar + (int64_t)bh * a.nq * D;
+  const float* kb = a.kbar + (int64_t)bh * a.nk * D;
+  float* so = a.score_out + (int64_t)bh * a.nq * a.nk;
+
+  float qa[DQ];
+  {
+    const int row = row0 + c;
+#pragma unroll
+    for (int s4 = 0; s4 < DQ / 4; ++s4) {
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (row < a.nq) v = *reinterpret_cast<const f32x4*>(qb + (int64_t)row * D + 16 * s4 + 4 * kg);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) qa[4 * s4 + u] = v[u];
+    }
+  }
+  f32x4 st[kLoads];
+  auto load_chunk = [&](int ch) {
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+      const int i = tid + 256 * u;
+      const int key = ch * KC + i / D4;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (key < a.nk) v = *reinterpret_cast<const f32x4*>(kb + (int64_t)key * D + 4 * (i % D4));
+      st[u] = v;
+    }
+  };
+  if (ch0 < ch1) load_chunk(ch0);
+  for (int ch = ch0; ch < ch1; ++ch) {
+    __syncthreads();  // the previous chunk is consumed
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+      const int i = tid + 256 * u;
+      *reinterpret_cast<f32x4*>(kch + (i / D4) * KS + 4 * (i % D4)) = st[u];
+    }
+    __syncthreads();
+    if (ch + 1 < ch1) load_chunk(ch + 1);
+    f32x4 acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < DQ / 4; ++s4) {
+      f32x4 kv[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        kv[t] = *reinterpret_cast<const f32x4*>(kch + (16 * t + c) * KS + 16 * s4 + 4 * kg);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * s4 + u], kv[t][u], acc[t], 0, 0, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int col = ch * KC + 16 * t + c;
+      if (col < a.nk) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + 4 * kg + i;
+          if (row < a.nq) so[(int64_t)row * a.nk + col] = acc[t][i];
+        }
+      }
+    }
+  }
+}
+
+template <int D>
+hipError_t launch_scores_mfma(RouteArgs a, int BH, hipStream_t stream) {
+  a.tiles_per_bh = (a.nq + 63) / 64;
+  const int nchunks = (a.nk + 63) / 64;
+  const int base = BH * a.tiles_per_bh;
+  int splits = (1024 + base - 1) / base;  // about four workgroups per CU
+  a.col_splits = splits < nchunks ? splits : nchunks;
+  hipLaunchKernelGGL((scores_kernel<D>), dim3(base * a.col_splits), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
 template <int NPER, int MODE>
 hipError_t launch_route_n(RouteArgs a, int BH, hipStream_t stream) {
-  constexpr int RW = NPER <= 16 ? 4 : (NPER == 32 ? 2 : 1);
+  // Score rows per wave: the top-k alone runs one row per wave (more rows in
+  // flight hide its serial search); with the score GEMM, up to 4 rows share
+  // each staged key chunk.
+  constexpr int RW = (MODE == kTopkOnly || NPER > 32) ? 1 : (NPER <= 16 ? 4 : 2);
   a.tiles_per_bh = (a.nq + 4 * RW - 1) / (4 * RW);
   hipLaunchKernelGGL((route_kernel<NPER, RW, MODE>), dim3(BH * a.tiles_per_bh), dim3(256), 0,
                      stream, a);
@@ -309,6 +487,10 @@ hipError_t launch_route_mfma(RouteArgs a, int BH, hipStream_t stream) {
 template <int MODE>
 hipError_t launch_route(RouteArgs a, int BH, hipStream_t stream) {
   const int per = (a.nk + 63) / 64;
+  if (MODE == kScoresOnly) {
+    if (a.D == 128) return launch_scores_mfma<128>(a, BH, stream);
+    if (a.D == 64) return launch_scores_mfma<64>(a, BH, stream);
+  }
   // Score GEMM on fp32 MFMA for the common head dims (score rows up to 2048
   // columns fit the LDS row buffer); the vector-ALU kernel covers the rest.
   if (MODE != kTopkOnly && per <= 32) {

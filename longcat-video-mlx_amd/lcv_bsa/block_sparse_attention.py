@@ -201,9 +201,13 @@ def topk_block_indices(
     return idx, k
 
 
-def select_block_indices(q_blocks: torch.Tensor, k_blocks: torch.Tensor, top_k: int) -> torch.Tensor:
-    """Fused ``topk_block_indices(block_routing_scores(q_blocks, k_blocks))``
-    without the score tensor (attention.py:105-108 in one kernel)."""
+def select_block_indices(q_blocks: torch.Tensor, k_blocks: torch.Tensor, top_k: int,
+                         *, fused: bool = False) -> torch.Tensor:
+    """``topk_block_indices(block_routing_scores(q_blocks, k_blocks))``
+    (attention.py:105-108).  By default in two kernels through a transient
+    fp32 score tensor (the faster route at 720p sizes); ``fused=True`` runs
+    the single kernel that keeps the scores on chip.  Both give the same
+    selection."""
     _require_device(q_blocks, k_blocks)
     qb = q_blocks.float().contiguous()
     kb = k_blocks.float().contiguous()
@@ -211,6 +215,8 @@ def select_block_indices(q_blocks: torch.Tensor, k_blocks: torch.Tensor, top_k: 
     nk = kb.shape[2]
     if not 1 <= top_k <= nk:
         raise ValueError(f"top_k={top_k} must be in [1, {nk}]")
+    if not fused:
+        return topk_block_indices(block_routing_scores(qb, kb), 0.0, top_k=top_k)[0]
     idx = torch.empty((B, H, nq, top_k), dtype=torch.int32, device=qb.device)
     st = _lib.load().lcv_bsa_select(qb.data_ptr(), kb.data_ptr(), B, H, nq, nk, D, top_k,
                                     idx.data_ptr(), _stream(qb))

@@ -90,7 +90,8 @@ def test_c_abi_validation_returns_before_launch():
     st = lib.lcv_bsa_select(fake, fake, 1, 1, 4, 8, 6, 4, fake, None)
     assert st == _lib.ERR_UNSUPPORTED  # D % 4
     ws = lib.lcv_bsa_forward_workspace_bytes(1, 32, 900, 128)
-    assert ws == 2 * 32 * 900 * 128 * 4 + (32 * 900 * 4 + 255) // 256 * 256
+    # pooled q and k means, block scores, launch order (each 256-byte aligned)
+    assert ws == 2 * 32 * 900 * 128 * 4 + 32 * 900 * 900 * 4 + (32 * 900 * 4 + 255) // 256 * 256
     st = lib.lcv_bsa_schedule(fake, 1, 1, 5000, 4, fake, None)
     assert st == _lib.ERR_UNSUPPORTED  # nq > 4096
     st = lib.lcv_bsa_forward(fake, fake, fake, 0, 1, 1, 4096, 128, S_(1 << 19, 1 << 19, 128),

@@ -150,6 +150,23 @@ def test_topk_exact_with_ties(device, nk):
         assert np.array_equal(got.cpu().numpy(), ref), f"nk={nk} k={k}"
 
 
+@pytest.mark.parametrize("nk", [64, 128, 129, 900, 2048])
+def test_topk_lower_bound_paths(device, nk):
+    """k on both sides of 64: the search over the keys above a lower bound
+    (the smallest of the lanes' largest keys) and the full search, on
+    continuous scores and with a third of some rows tied at the top."""
+    from lcv_bsa import topk_block_indices
+
+    rng = np.random.default_rng(100 + nk)
+    sc = rng.standard_normal((1, 2, 9, nk)).astype(np.float32)
+    sc[0, 1, :3, : nk // 3] = 5.0
+    sct = torch.from_numpy(sc).to(device)
+    for k in sorted({1, 2, 57, 63, 64, 65, 100, 127, 128, 129} & set(range(1, nk + 1))):
+        got, _ = topk_block_indices(sct, 0.0, top_k=k)
+        ref, _ = O.topk_block_indices(sc, top_k=k)
+        assert np.array_equal(got.cpu().numpy(), ref), f"nk={nk} k={k}"
+
+
 def test_topk_count_rule(device):
     """test_bsa_tier_a_smoke.py:78-94 on the HIP top-k."""
     from lcv_bsa import topk_block_indices
@@ -171,13 +188,14 @@ def test_select_fused_equals_two_step(device, nq, nk, D, k):
 
     qb = _rand((1, 2, nq, D), torch.float32, device, seed=3 * nq)
     kb = _rand((1, 2, nk, D), torch.float32, device, seed=5 * nk)
-    fused = select_block_indices(qb, kb, k)
+    fused = select_block_indices(qb, kb, k, fused=True)
     two, _ = topk_block_indices(block_routing_scores(qb, kb), 0.0, top_k=k)
     assert torch.equal(fused, two)
+    assert torch.equal(select_block_indices(qb, kb, k), two)
     qi, ki = torch.round(qb * 2), torch.round(kb * 2)
-    fused_i = select_block_indices(qi, ki, k).cpu().numpy()
     ref, _ = O.topk_block_indices(O.block_routing_scores(_np(qi), _np(ki)), top_k=k)
-    assert np.array_equal(fused_i, ref)
+    for f in (True, False):
+        assert np.array_equal(select_block_indices(qi, ki, k, fused=f).cpu().numpy(), ref)
 
 
 # ---------------------------------------------------------------------------
