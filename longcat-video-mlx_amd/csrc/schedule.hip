@@ -58,12 +58,64 @@ __global__ __launch_bounds__(256) void schedule_kernel(const int32_t* idx, int n
     order[(int64_t)bh * nq + i] = (int32_t)(keys[i] & 0xFFFFFu);
 }
 
+// The same sort for nq <= 1024 with one key per thread: the 45 of 55
+// bitonic stages whose partner lies in the same wave (j < 64) exchange keys
+// with lane shuffles; only the 10 with j >= 64 go through LDS and barriers.
+constexpr int kSmallSched = 1024;
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int m) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, m);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__global__ __launch_bounds__(kSmallSched) void schedule_small_kernel(const int32_t* idx, int nq,
+                                                                     int top_k, int32_t* order) {
+  __shared__ uint64_t xch[kSmallSched];
+  const int bh = blockIdx.x;
+  const int i = threadIdx.x;
+  const int32_t* rows = idx + (int64_t)bh * nq * top_k;
+  const int mid = top_k / 2;
+  uint64_t key = ~0ull;  // padding sorts last
+  if (i < nq) {
+    int first = rows[(int64_t)i * top_k];
+    int median = rows[(int64_t)i * top_k + mid];
+    first = (first < 0 || first >= nq) ? nq : first;
+    median = (median < 0 || median >= nq) ? nq : median;
+    key = ((uint64_t)first << 40) | ((uint64_t)median << 20) | (uint64_t)i;
+  }
+  for (int k = 2; k <= kSmallSched; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      uint64_t other;
+      if (j < 64) {
+        other = shfl_xor_u64(key, j);
+      } else {
+        xch[i] = key;
+        __syncthreads();
+        other = xch[i ^ j];
+        __syncthreads();
+      }
+      const bool up = (i & k) == 0;
+      const bool lower = (i & j) == 0;  // i < i ^ j
+      const uint64_t lo = other < key ? other : key;
+      const uint64_t hi = other < key ? key : other;
+      key = (lower == up) ? lo : hi;
+    }
+  }
+  if (i < nq) order[(int64_t)bh * nq + i] = (int32_t)(key & 0xFFFFFu);
+}
+
 }  // namespace
 
 bool schedule_supported(int nq) { return nq >= 1 && nq <= kMaxSched; }
 
 hipError_t launch_schedule(const int32_t* idx, int BH, int nq, int top_k, int32_t* order,
                            hipStream_t stream) {
+  if (nq <= kSmallSched) {
+    hipLaunchKernelGGL(schedule_small_kernel, dim3(BH), dim3(kSmallSched), 0, stream, idx, nq,
+                       top_k, order);
+    return hipGetLastError();
+  }
   int n = 1;
   while (n < nq) n <<= 1;
   hipLaunchKernelGGL(schedule_kernel, dim3(BH), dim3(256), 0, stream, idx, nq, top_k, n, order);
