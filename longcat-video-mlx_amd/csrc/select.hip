@@ -257,17 +257,15 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
 // dim 16 s4 + 4 kg + u of q-block row c (A) and of key row 16t + c (B), so
 // the four kg lanes of a row load 64 contiguous bytes per instruction (16
 // cache lines per wave load, not 64).  The accumulator holds
-// S[4kg + i][16t + c].  kSelect
-// gathers the 16 x nk rows in LDS and runs wave_topk on them; kScoresOnly
-// writes the tiles to global memory.
-template <int NPER, int MODE, int D>
-__global__ __launch_bounds__(256) void route_mfma_kernel(RouteArgs a) {
+// S[4kg + i][16t + c].  The 16 x nk score rows are gathered in LDS and each
+// wave runs wave_topk on four of them: routing without a score buffer.
+template <int NPER, int D>
+__global__ __launch_bounds__(256) void select_mfma_kernel(RouteArgs a) {
   constexpr int QR = 16;
   constexpr int DQ = D / 4;                 // dims per lane group
   constexpr int LDSW = NPER * 64 + 4;       // score row stride (floats)
-  constexpr int kLds = MODE == kSelect ? QR * LDSW : 1;
-  __shared__ __attribute__((aligned(16))) float srow[kLds];
-  __shared__ uint32_t tk_buf[MODE == kSelect ? 4 : 1][MODE == kSelect ? kCompactCap : 1];
+  __shared__ __attribute__((aligned(16))) float srow[QR * LDSW];
+  __shared__ uint32_t tk_buf[4][kCompactCap];
   const int tid = threadIdx.x;
   const int wave = tid / 64;
   const int lane = tid % 64;
@@ -308,18 +306,8 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(RouteArgs a) {
 #pragma unroll
     for (int s = 0; s < DQ; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], kv[s], acc, 0, 0, 0);
     const int col = 16 * tt + c;
-    if (MODE == kSelect) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) srow[(4 * kg + i) * LDSW + col] = acc[i];
-    } else {
-      if (col < a.nk) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = row0 + 4 * kg + i;
-          if (row < a.nq) a.score_out[((int64_t)bh * a.nq + row) * a.nk + col] = acc[i];
-        }
-      }
-    }
+    for (int i = 0; i < 4; ++i) srow[(4 * kg + i) * LDSW + col] = acc[i];
   };
   for (; t < ntiles; t += 8) {
     if (t + 4 < ntiles) load_b(t + 4, kv1);
@@ -328,18 +316,16 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(RouteArgs a) {
     if (t + 8 < ntiles) load_b(t + 8, kv0);
     tile(t + 4, kv1);
   }
-  if (MODE == kSelect) {
-    __syncthreads();
+  __syncthreads();
 #pragma unroll 1
-    for (int r = wave; r < QR; r += 4) {
-      const int row = row0 + r;
-      if (row >= a.nq) break;  // wave-uniform; rows only grow
-      float sc[NPER];
+  for (int r = wave; r < QR; r += 4) {
+    const int row = row0 + r;
+    if (row >= a.nq) break;  // wave-uniform; rows only grow
+    float sc[NPER];
 #pragma unroll
-      for (int e = 0; e < NPER; ++e) sc[e] = srow[r * LDSW + e * 64 + lane];
-      wave_topk<NPER>(sc, a.nk, a.top_k, a.idx + ((int64_t)bh * a.nq + row) * a.top_k,
-                      tk_buf[wave]);
-    }
+    for (int e = 0; e < NPER; ++e) sc[e] = srow[r * LDSW + e * 64 + lane];
+    wave_topk<NPER>(sc, a.nk, a.top_k, a.idx + ((int64_t)bh * a.nq + row) * a.top_k,
+                    tk_buf[wave]);
   }
 }
 
@@ -465,23 +451,23 @@ hipError_t launch_route_n(RouteArgs a, int BH, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int NPER, int MODE, int D>
-hipError_t launch_route_mfma_n(RouteArgs a, int BH, hipStream_t stream) {
+template <int NPER, int D>
+hipError_t launch_select_mfma_n(RouteArgs a, int BH, hipStream_t stream) {
   a.tiles_per_bh = (a.nq + 15) / 16;
-  hipLaunchKernelGGL((route_mfma_kernel<NPER, MODE, D>), dim3(BH * a.tiles_per_bh), dim3(256), 0,
+  hipLaunchKernelGGL((select_mfma_kernel<NPER, D>), dim3(BH * a.tiles_per_bh), dim3(256), 0,
                      stream, a);
   return hipGetLastError();
 }
 
-template <int MODE, int D>
-hipError_t launch_route_mfma(RouteArgs a, int BH, hipStream_t stream) {
+template <int D>
+hipError_t launch_select_mfma(RouteArgs a, int BH, hipStream_t stream) {
   const int per = (a.nk + 63) / 64;
-  if (per <= 1) return launch_route_mfma_n<1, MODE, D>(a, BH, stream);
-  if (per <= 2) return launch_route_mfma_n<2, MODE, D>(a, BH, stream);
-  if (per <= 4) return launch_route_mfma_n<4, MODE, D>(a, BH, stream);
-  if (per <= 8) return launch_route_mfma_n<8, MODE, D>(a, BH, stream);
-  if (per <= 16) return launch_route_mfma_n<16, MODE, D>(a, BH, stream);
-  return launch_route_mfma_n<32, MODE, D>(a, BH, stream);
+  if (per <= 1) return launch_select_mfma_n<1, D>(a, BH, stream);
+  if (per <= 2) return launch_select_mfma_n<2, D>(a, BH, stream);
+  if (per <= 4) return launch_select_mfma_n<4, D>(a, BH, stream);
+  if (per <= 8) return launch_select_mfma_n<8, D>(a, BH, stream);
+  if (per <= 16) return launch_select_mfma_n<16, D>(a, BH, stream);
+  return launch_select_mfma_n<32, D>(a, BH, stream);
 }
 
 template <int MODE>
@@ -491,11 +477,12 @@ hipError_t launch_route(RouteArgs a, int BH, hipStream_t stream) {
     if (a.D == 128) return launch_scores_mfma<128>(a, BH, stream);
     if (a.D == 64) return launch_scores_mfma<64>(a, BH, stream);
   }
-  // Score GEMM on fp32 MFMA for the common head dims (score rows up to 2048
-  // columns fit the LDS row buffer); the vector-ALU kernel covers the rest.
-  if (MODE != kTopkOnly && per <= 32) {
-    if (a.D == 128) return launch_route_mfma<MODE, 128>(a, BH, stream);
-    if (a.D == 64) return launch_route_mfma<MODE, 64>(a, BH, stream);
+  // Fused routing on fp32 MFMA for the common head dims (score rows up to
+  // 2048 columns fit the LDS row buffer); the vector-ALU kernel covers the
+  // rest.
+  if (MODE == kSelect && per <= 32) {
+    if (a.D == 128) return launch_select_mfma<128>(a, BH, stream);
+    if (a.D == 64) return launch_select_mfma<64>(a, BH, stream);
   }
   if (per <= 1) return launch_route_n<1, MODE>(a, BH, stream);
   if (per <= 2) return launch_route_n<2, MODE>(a, BH, stream);
