@@ -678,7 +678,9 @@ bool attn_uses_mfma(int dtype, int D) {
 }
 
 bool attn_supported(int dtype, int D) {
-  return D == 16 || D == 32 || D == 64 || D == 128 || D == 256;
+  // Every dtype has the vector-ALU kernel at these head dims.
+  const bool dtype_ok = dtype == LCV_BSA_F16 || dtype == LCV_BSA_BF16 || dtype == LCV_BSA_F32;
+  return dtype_ok && (D == 16 || D == 32 || D == 64 || D == 128 || D == 256);
 }
 
 hipError_t launch_attn(const AttnParams& p, int dtype, int D, hipStream_t stream) {
