@@ -9,58 +9,51 @@
 // work ids land on the same XCD (xcd_linear_work_id), so the sorted runs
 // execute together.
 //
-// One workgroup per (b, h): keys are built from idx[b,h,i,0] and
-// idx[b,h,i,top_k/2] (entries outside [0, nq) count as nq) and bitonic-sorted
-// in LDS together with the q-block index, which also makes the order a
-// permutation.
+// q-block i's key is (first, median, i), entries outside [0, nq) counting as
+// nq.  The key is unique, so the sorted order is a permutation, the same one
+// any correct sort gives.  Two sorts:
+//   * nq <= 1024: one workgroup per head, one key per thread, bitonic; the
+//     stages whose partner lies in the same wave exchange keys with lane
+//     shuffles, the rest through LDS;
+//   * 1024 < nq <= 4096: a rank sort.  i goes to position #{j : key_j <
+//     key_i}; every workgroup stages all keys of its head in LDS and ranks 256
+//     of them, one per thread, in one pass over the staged keys (broadcast
+//     LDS reads, no barriers after the staging), so a head's sort spreads
+//     over ceil(nq / 256) workgroups instead of 78 dependent bitonic stages.
 #include "bsa_common.h"
 
 namespace lcv {
 namespace {
 
 constexpr int kMaxSched = 4096;
+constexpr int kRankThreads = 256;
 
-__global__ __launch_bounds__(256) void schedule_kernel(const int32_t* idx, int nq, int top_k,
-                                                       int n_pow2, int32_t* order) {
+__global__ __launch_bounds__(kRankThreads) void schedule_rank_kernel(const int32_t* idx, int nq,
+                                                                     int top_k, int32_t* order) {
   __shared__ uint64_t keys[kMaxSched];
   const int bh = blockIdx.x;
   const int32_t* rows = idx + (int64_t)bh * nq * top_k;
   const int mid = top_k / 2;
-  for (int i = threadIdx.x; i < n_pow2; i += 256) {
-    uint64_t key = ~0ull;  // padding sorts last
-    if (i < nq) {
-      int first = rows[(int64_t)i * top_k];
-      int median = rows[(int64_t)i * top_k + mid];
-      first = (first < 0 || first >= nq) ? nq : first;
-      median = (median < 0 || median >= nq) ? nq : median;
-      key = ((uint64_t)first << 40) | ((uint64_t)median << 20) | (uint64_t)i;
-    }
-    keys[i] = key;
+  for (int i = threadIdx.x; i < nq; i += kRankThreads) {
+    int first = rows[(int64_t)i * top_k];
+    int median = rows[(int64_t)i * top_k + mid];
+    first = (first < 0 || first >= nq) ? nq : first;
+    median = (median < 0 || median >= nq) ? nq : median;
+    keys[i] = ((uint64_t)first << 40) | ((uint64_t)median << 20) | (uint64_t)i;
   }
   __syncthreads();
-  for (int k = 2; k <= n_pow2; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < n_pow2; i += 256) {
-        const int p = i ^ j;
-        if (p > i) {
-          const uint64_t a = keys[i], b = keys[p];
-          const bool up = (i & k) == 0;
-          if ((a > b) == up) {
-            keys[i] = b;
-            keys[p] = a;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-  for (int i = threadIdx.x; i < nq; i += 256)
-    order[(int64_t)bh * nq + i] = (int32_t)(keys[i] & 0xFFFFFu);
+  const int i = blockIdx.y * kRankThreads + threadIdx.x;
+  if (i >= nq) return;
+  const uint64_t mine = keys[i];
+  int rank = 0;
+#pragma unroll 8
+  for (int j = 0; j < nq; ++j) rank += keys[j] < mine ? 1 : 0;
+  order[(int64_t)bh * nq + rank] = i;
 }
 
-// The same sort for nq <= 1024 with one key per thread: the 45 of 55
-// bitonic stages whose partner lies in the same wave (j < 64) exchange keys
-// with lane shuffles; only the 10 with j >= 64 go through LDS and barriers.
+// The bitonic sort for nq <= 1024 with one key per thread: the 45 of 55
+// stages whose partner lies in the same wave (j < 64) exchange keys with lane
+// shuffles; only the 10 with j >= 64 go through LDS and barriers.
 constexpr int kSmallSched = 1024;
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int m) {
@@ -111,14 +104,15 @@ bool schedule_supported(int nq) { return nq >= 1 && nq <= kMaxSched; }
 
 hipError_t launch_schedule(const int32_t* idx, int BH, int nq, int top_k, int32_t* order,
                            hipStream_t stream) {
+  if (!schedule_supported(nq) || BH < 1 || top_k < 1) return hipErrorInvalidValue;
   if (nq <= kSmallSched) {
     hipLaunchKernelGGL(schedule_small_kernel, dim3(BH), dim3(kSmallSched), 0, stream, idx, nq,
                        top_k, order);
     return hipGetLastError();
   }
-  int n = 1;
-  while (n < nq) n <<= 1;
-  hipLaunchKernelGGL(schedule_kernel, dim3(BH), dim3(256), 0, stream, idx, nq, top_k, n, order);
+  const dim3 grid((unsigned)BH, (unsigned)((nq + kRankThreads - 1) / kRankThreads));
+  hipLaunchKernelGGL(schedule_rank_kernel, grid, dim3(kRankThreads), 0, stream, idx, nq, top_k,
+                     order);
   return hipGetLastError();
 }
 

@@ -361,8 +361,9 @@ def _attn_with_order(q, k, v, idx, shape, chunk, order):
 
 @pytest.mark.parametrize("nb,k", [(1, 1), (7, 3), (64, 4), (900, 57), (1024, 8), (1025, 8), (4096, 5)])
 def test_schedule_permutation_sorted_by_key(device, nb, k):
-    """Both sorts: one key per thread with lane shuffles (nb <= 1024) and the
-    LDS bitonic sort above."""
+    """Both sorts: the in-wave bitonic sort (nb <= 1024) and the rank sort
+    over several workgroups per head (1024 < nb <= 4096); padded entries
+    count as nb."""
     from lcv_bsa import schedule_block_order
 
     idx = np.sort(_distinct_indices(1, 2, nb, nb, k, seed=nb), axis=-1)
