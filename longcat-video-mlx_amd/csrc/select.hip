@@ -402,26 +402,47 @@ __global__ __launch_bounds__(256) void scores_kernel(RouteArgs a) {
     f32x4 acc[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < DQ / 4; ++s4) {
-      f32x4 kv[4];
+    // The key operands of step s4 + 1 are read while the MFMAs of step s4
+    // run (scheduling groups keep the compiler from sinking the reads).
+    f32x4 kv[2][4];
+    auto read_kv = [&](int s4, f32x4* dst) {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        kv[t] = *reinterpret_cast<const f32x4*>(kch + (16 * t + c) * KS + 16 * s4 + 4 * kg);
+        dst[t] = *reinterpret_cast<const f32x4*>(kch + (16 * t + c) * KS + 16 * s4 + 4 * kg);
+    };
+    read_kv(0, kv[0]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+    for (int s4 = 0; s4 < DQ / 4; ++s4) {
+      if (s4 + 1 < DQ / 4) read_kv(s4 + 1, kv[(s4 + 1) & 1]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * s4 + u], kv[t][u], acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * s4 + u], kv[s4 & 1][t][u], acc[t], 0,
+                                                        0, 0);
+        if (s4 + 1 < DQ / 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA
+      }
     }
+    // Scores: rows row0 + 4kg + i, columns ch*64 + 16t + c.  Interior tiles
+    // store without per-element checks.
+    float* srow = so + (int64_t)(row0 + 4 * kg) * a.nk + ch * KC + c;
+    if (row0 + 16 <= a.nq && (ch + 1) * KC <= a.nk) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int col = ch * KC + 16 * t + c;
-      if (col < a.nk) {
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = row0 + 4 * kg + i;
-          if (row < a.nq) so[(int64_t)row * a.nk + col] = acc[t][i];
+        for (int t = 0; t < 4; ++t) srow[(int64_t)i * a.nk + 16 * t] = acc[t][i];
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int col = ch * KC + 16 * t + c;
+        if (col < a.nk) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int row = row0 + 4 * kg + i;
+            if (row < a.nq) so[(int64_t)row * a.nk + col] = acc[t][i];
+          }
         }
       }
     }
