@@ -448,8 +448,10 @@ void attn_mfma_kernel(AttnParams p) {
     // P^T as the B operand: step s takes accumulator values 8s .. 8s+7, the
     // key runs 16s + 4g + {0..3} and 16s + 8 + 4g + {0..3}.
     vec8 pf[4];
+    // The row sum is kept as four partial sums (one per PV step), so its
+    // dot products form four short dependency chains instead of one long one.
     auto exps = [&]() {
-      float ls = 0.0f;
+      float ls[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
 #pragma unroll
@@ -457,9 +459,9 @@ void attn_mfma_kernel(AttnParams p) {
           const int flat = 8 * s + jj;
           pf[s][jj] = from_f32<T>(fast_exp2(fmaf(sacc[flat / 16][flat % 16], sl2, -m_run)));
         }
-        ls = Mfma<T>::sum8(pf[s], ls);
+        ls[s] = Mfma<T>::sum8(pf[s], 0.0f);
       }
-      return ls;
+      return (ls[0] + ls[2]) + (ls[1] + ls[3]);
     };
     if (first) m_run = rowmax();  // wave-uniform; O and l are still 0
     float ls = exps();
