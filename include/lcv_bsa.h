@@ -128,7 +128,9 @@ int lcv_bsa_schedule(const int32_t* idx, int64_t B, int64_t H, int64_t nq,
  * gets zeros.  Duplicate entries are attended once per occurrence (the
  * reference kernels' behaviour).  idx is a dense [B,H,nb,top_k] int32.
  * order (nullable) is a per-head permutation of the q-blocks giving the
- * launch order (lcv_bsa_schedule); null launches in block order.
+ * launch order (lcv_bsa_schedule); null launches in block order.  An order
+ * entry outside [0, nb) launches nothing (that slot's work is skipped, so a
+ * non-permutation leaves some output rows unwritten).
  * Blocks must hold 64 tokens.  D in {16,32,64,128,256} (MFMA path for
  * fp16/bf16 with D in {64,128}; other combinations use a vector-ALU path).
  * Replaces bsa_attention_metal_v4 / _v3 / _v2 / bsa_attention_metal,

@@ -248,6 +248,7 @@ void attn_mfma_kernel(AttnParams p) {
   const int wid = xcd_linear_work_id(blockIdx.x, gridDim.x);
   const int bh = wid / p.nb;
   const int qb = p.order ? uniform_i32(p.order[wid]) : wid - bh * p.nb;
+  if ((uint32_t)qb >= (uint32_t)p.nb) return;  // a launch-order entry outside [0, nb): nothing to do
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int tid = threadIdx.x;
@@ -577,6 +578,7 @@ __global__ __launch_bounds__(256) void attn_valu_kernel(AttnParams p) {
   const int wid = xcd_linear_work_id(blockIdx.x, gridDim.x);
   const int bh = wid / p.nb;
   const int qb = p.order ? uniform_i32(p.order[wid]) : wid - bh * p.nb;
+  if ((uint32_t)qb >= (uint32_t)p.nb) return;  // a launch-order entry outside [0, nb): nothing to do
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int tid = threadIdx.x;

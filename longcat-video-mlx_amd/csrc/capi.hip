@@ -54,17 +54,21 @@ int check_geom(int64_t B, int64_t H, int64_t S, int64_t D, const lcv_bsa_geom& g
                 (long long)B, (long long)H, (long long)S, (long long)D);
   if (g.T <= 0 || g.Hl <= 0 || g.Wl <= 0 || g.cT <= 0 || g.cH <= 0 || g.cW <= 0)
     return fail(LCV_BSA_ERR_INVALID_ARG, "grid and chunk extents must be positive");
+  // Bound every factor before the products below (no int64 overflow).
+  if (S > kI32Max / 2 || B > kI32Max || H > kI32Max || D > kI32Max || g.T > kI32Max ||
+      g.Hl > kI32Max || g.Wl > kI32Max || g.cT > kI32Max || g.cH > kI32Max || g.cW > kI32Max)
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "S=%lld or an extent beyond 2^31", (long long)S);
   if (g.T % g.cT || g.Hl % g.cH || g.Wl % g.cW)
     return fail(LCV_BSA_ERR_SHAPE,
                 "Latent shape (%lld, %lld, %lld) must be a multiple of chunk_thw (%lld, %lld, %lld)",
                 (long long)g.T, (long long)g.Hl, (long long)g.Wl, (long long)g.cT, (long long)g.cH,
                 (long long)g.cW);
-  if (S != g.T * g.Hl * g.Wl)
-    return fail(LCV_BSA_ERR_SHAPE, "S=%lld doesn't match T*H*W=%lld", (long long)S,
-                (long long)(g.T * g.Hl * g.Wl));
-  if (S > kI32Max / 2 || B * H > kI32Max / 4)
-    return fail(LCV_BSA_ERR_UNSUPPORTED, "S=%lld or B*H=%lld too large", (long long)S,
-                (long long)(B * H));
+  const int64_t thw = g.T * g.Hl > S ? -1 : g.T * g.Hl * g.Wl;  // factors < 2^31: no overflow
+  if (S != thw)
+    return fail(LCV_BSA_ERR_SHAPE, "S=%lld doesn't match T*H*W=%lld*%lld*%lld", (long long)S,
+                (long long)g.T, (long long)g.Hl, (long long)g.Wl);
+  if (B * H > kI32Max / 4)
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "B*H=%lld too large", (long long)(B * H));
   *bs = g.cT * g.cH * g.cW;
   *nb = S / *bs;
   if (B * H * (*nb) > kI32Max)

@@ -62,6 +62,15 @@ def test_c_abi_validation_returns_before_launch():
     assert st == _lib.ERR_SHAPE and b"doesn't match" in lib.lcv_bsa_last_error()
     st = lib.lcv_bsa_pool(fake, 7, 1, 1, 64, 8, S_(512, 512, 8), G(4, 4, 4, 4, 4, 4), fake, None)
     assert st == _lib.ERR_DTYPE
+    # Extents whose product overflows int64: rejected, not wrapped into a match.
+    big = 1 << 40
+    st = lib.lcv_bsa_pool(fake, 0, 1, 1, 64, 8, S_(512, 512, 8), G(big, big, 1 << 24, 4, 4, 4), fake, None)
+    assert st == _lib.ERR_UNSUPPORTED
+    st = lib.lcv_bsa_pool(fake, 0, 1, 1, 1 << 20, 8, S_(512, 512, 8),
+                          G(1 << 30, 1 << 30, 4, 4, 4, 4), fake, None)
+    assert st == _lib.ERR_SHAPE and b"doesn't match" in lib.lcv_bsa_last_error()
+    st = lib.lcv_bsa_pool(fake, 0, big, big, 64, 8, S_(512, 512, 8), G(4, 4, 4, 4, 4, 4), fake, None)
+    assert st == _lib.ERR_UNSUPPORTED
     args = dict(B=1, H=1, S=64, D=128)
     st = lib.lcv_bsa_attn_fwd(fake, fake, fake, 0, 1, 1, 64, 128, S_(8192, 8192, 128),
                               S_(8192, 8192, 128), S_(8192, 8192, 128), fake, None, 0, 0.1,

@@ -343,12 +343,12 @@ def test_block_major_permutation_exact(device, dtype):
 # Launch order (scheduling): a permutation; results independent of it
 # ---------------------------------------------------------------------------
 
-def _attn_with_order(q, k, v, idx, shape, chunk, order):
+def _attn_with_order(q, k, v, idx, shape, chunk, order, out=None):
     from lcv_bsa import _lib
     from lcv_bsa.block_sparse_attention import _geom, _strides
 
     B, H, S, D = q.shape
-    out = torch.empty_like(q)
+    out = torch.empty_like(q) if out is None else out
     st = _lib.load().lcv_bsa_attn_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), {torch.float16: 0, torch.bfloat16: 1,
                                                    torch.float32: 2}[q.dtype],
@@ -401,6 +401,27 @@ def test_attention_launch_order_changes_only_rounding(device, dtype):
     for name in ("schedule", "random"):
         d = (outs[name].float() - outs["identity"].float()).abs().max().item()
         assert d <= 4 * ulp, f"order={name}: max |diff| {d:.3g} > 4 ulp"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_attention_launch_order_out_of_range_entries_launch_nothing(device, dtype):
+    """A launch-order entry outside [0, nb) launches nothing: the q-block it
+    would have named keeps what the output held, every other q-block is
+    computed as usual (MFMA path for fp16, vector-ALU path for fp32)."""
+    shape, chunk = (1, 1, 1024), (1, 1, 64)
+    D = 128 if dtype != torch.float32 else 64
+    q, k, v = (_rand((1, 2, 1024, D), dtype, device, seed=s) for s in (41, 42, 43))
+    idx = torch.from_numpy(np.sort(_distinct_indices(1, 2, 16, 16, 4, seed=6), axis=-1)).to(device)
+    ref = O.sparse_attention_from_indices(_np(q), _np(k), _np(v), idx.cpu().numpy(), shape, chunk)
+    order = torch.arange(16, dtype=torch.int32).repeat(1, 2, 1)
+    order[0, 0, 3] = 16  # q-block 3 of head 0 is never launched
+    order[0, 1, 5] = -7  # q-block 5 of head 1 is never launched
+    out = torch.full_like(q, 7.0)
+    _attn_with_order(q, k, v, idx, shape, chunk, order.to(device), out=out)
+    expect = ref.copy()
+    expect[0, 0, 3 * 64:4 * 64] = 7.0
+    expect[0, 1, 5 * 64:6 * 64] = 7.0
+    assert_close_report(_np(out), expect, *TOL[dtype], f"attn order with skipped entries {dtype}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
