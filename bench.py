@@ -540,6 +540,18 @@ def main() -> int:
     torch.cuda.synchronize()
     ms_step = ev0.elapsed_time(ev1) / args.steps
 
+    # The same forwards with an event between each: the median latency of
+    # one forward (the timed loop above gives the throughput).
+    evf = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    torch.cuda.synchronize()
+    evf[0].record(stream)
+    for i in range(args.steps):
+        forward()
+        evf[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per_fwd = sorted(evf[i].elapsed_time(evf[i + 1]) for i in range(args.steps))
+    ms_median = per_fwd[len(per_fwd) // 2] if len(per_fwd) % 2 else 0.5 * (per_fwd[len(per_fwd) // 2 - 1] + per_fwd[len(per_fwd) // 2])
+
     # Timed region 2: the same work stage by stage, events between stages.
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
     torch.cuda.synchronize()
@@ -561,7 +573,7 @@ def main() -> int:
     attn_tflops = flops / (ms_attn * 1e-3) / 1e12
     peak = PEAK_TFLOPS.get(dtype, 2500.0)
     workload = f"{args.config}_k{top_k}"
-    log(f"forward {ms_step:.3f} ms ({tflops:.1f} TFLOP/s executed-block); pool {ms_pool:.3f} ms, "
+    log(f"forward {ms_step:.3f} ms (median {ms_median:.3f}; {tflops:.1f} TFLOP/s executed-block); pool {ms_pool:.3f} ms, "
         f"select {ms_sel:.3f} ms, attention {ms_attn:.3f} ms ({attn_tflops:.1f} TFLOP/s, "
         f"{100 * attn_tflops / peak:.1f}% of {peak:.0f})")
 
@@ -573,6 +585,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
+        "ms_forward_median": round(ms_median, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
