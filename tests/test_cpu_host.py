@@ -421,3 +421,18 @@ def test_dit_block_reference_modulation_asserts_fp32():
     assert torch.allclose(y, torch.nn.functional.layer_norm(x, (8,), eps=1e-6), atol=1e-6)
     with pytest.raises(AssertionError):
         modulate_fp32(norm, x, zero.to(torch.bfloat16), zero)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py runs the single-GPU path only: --gpus 2 exits with status 2
+    and says why, before touching a device."""
+    import json
+    import subprocess
+    import sys
+
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], cwd=root,
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    msg = json.loads(r.stdout.strip().splitlines()[-1])
+    assert "one GPU" in msg["error"]
