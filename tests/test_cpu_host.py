@@ -436,3 +436,21 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2
     msg = json.loads(r.stdout.strip().splitlines()[-1])
     assert "one GPU" in msg["error"]
+
+
+@pytest.mark.parametrize("lang,std", [("c", "c99"), ("c++", "c++17")])
+def test_header_compiles_for_c_and_cpp_callers(tmp_path, lang, std):
+    """include/lcv_bsa.h is a plain C-ABI header: it compiles warning-free as
+    C99 and as C++17 (the bindings of a cgo / JNI / N-API / ctypes caller)."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc" if lang == "c" else "g++")
+    if cc is None:
+        pytest.skip("no host compiler")
+    src = tmp_path / "use_header.c"
+    src.write_text('#include "lcv_bsa.h"\nint main(void) { return lcv_bsa_version() ? 0 : 1; }\n')
+    r = subprocess.run([cc, "-x", lang, f"-std={std}", "-Wall", "-Wextra", "-pedantic", "-Werror",
+                        f"-I{REPO / 'include'}", "-fsyntax-only", str(src)],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
