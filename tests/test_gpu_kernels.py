@@ -228,6 +228,31 @@ def test_attn_matches_oracle(device, dtype, D, geom):
         assert_close_report(_np(out), ref, *TOL[dtype], f"attn {dtype} D={D} {geom} k={topk}")
 
 
+@pytest.mark.parametrize("dtype,topk", [(torch.float16, 129), (torch.bfloat16, 100)])
+def test_attn_lists_longer_than_64(device, dtype, topk):
+    """Routing lists of more than 64 entries: the tile walk reads them in
+    64-entry chunks and starts each q-block's walk at a launch-slot-dependent
+    entry, so with 8 heads x 130 q-blocks (1040 workgroups) the start lands
+    in the second chunk for some of them and the walk wraps around.  Some
+    rows carry padding (-1) in the second chunk and some are unsorted."""
+    from lcv_bsa import bsa_attention_hip
+
+    H, nb, D = 8, 130, 128
+    S = nb * 64
+    shape, chunk = (1, 1, S), (1, 1, 64)
+    q, k, v = (_rand((1, H, S, D), dtype, device, seed=s) for s in (51, 52, 53))
+    rng = np.random.default_rng(topk)
+    idx = _distinct_indices(1, H, nb, nb, topk, seed=topk)
+    for h in range(H):
+        for r in rng.choice(nb, 6, replace=False):
+            idx[0, h, r, 70 + rng.integers(0, topk - 70):] = -1  # padding in the second chunk
+        for r in rng.choice(nb, 6, replace=False):
+            rng.shuffle(idx[0, h, r])  # the walk does not rely on order for correctness
+    out = bsa_attention_hip(q, k, v, torch.from_numpy(idx).to(device), chunk, shape)
+    ref = O.sparse_attention_from_indices(_np(q), _np(k), _np(v), idx, shape, chunk)
+    assert_close_report(_np(out), ref, *TOL[dtype], f"attn top-k {topk} > 64 {dtype}")
+
+
 @pytest.mark.parametrize("D", [16, 32, 256])
 def test_attn_valu_head_dims(device, D):
     from lcv_bsa import bsa_attention_hip
