@@ -9,8 +9,14 @@ Mirrors ``Attention._process_attn`` (longcat_video/models/attention.py:71-179):
 * the dense path uses ``scale = head_dim ** -0.5`` (attention.py:49, 179).
 
 Backends: ``"hip"`` is this package's gfx950 path.  The reference's own
-backend names (``tier_a``, ``metal*``) need MLX on Apple hardware and are
-rejected with a clear error rather than silently remapped.
+backend names (``"tier_a"``, ``"metal"``, ``"metal_v2"``, ``"metal_v3"``,
+``"metal_v4"``; longcat_video_dit.py:249-252) are accepted and run the same
+HIP kernels: on the reference they are implementations of one function
+(Tier A's masked dense SDPA and the Metal kernels give the same output up to
+rounding, bsa.py:201-250, metal.py:75-1046), so an unchanged caller --
+``enable_bsa()`` with its default ``"tier_a"``, or scripts/run_refine.py
+with ``LONGCAT_BSA_BACKEND`` unset -- gets BSA on MI355X.  The name is kept
+on the layer as given; ``resolve_backend`` says which path serves it.
 """
 
 from __future__ import annotations
@@ -24,28 +30,37 @@ import torch.nn.functional as F
 from .block_sparse_attention import bsa_attention
 
 ENV_VAR = "LONGCAT_BSA_BACKEND"
-DEFAULT_BACKEND = "hip"
-VALID_BACKENDS = ("hip",)
-REFERENCE_ONLY_BACKENDS = ("tier_a", "metal", "metal_v2", "metal_v3", "metal_v4")
+# The reference's default name (longcat_video_dit.py:219, attention.py:69,
+# scripts/run_refine.py:91); it resolves to the HIP path.
+DEFAULT_BACKEND = "tier_a"
+# Names the reference accepts (longcat_video_dit.py:249), each served here by
+# the HIP kernels, plus this package's own name.
+REFERENCE_BACKENDS = ("tier_a", "metal", "metal_v2", "metal_v3", "metal_v4")
+VALID_BACKENDS = ("hip",) + REFERENCE_BACKENDS
 
 __all__ = [
-    "BSAAttention", "ENV_VAR", "DEFAULT_BACKEND", "VALID_BACKENDS", "REFERENCE_ONLY_BACKENDS",
-    "backend_from_env", "validate_backend", "dense_attention",
+    "BSAAttention", "ENV_VAR", "DEFAULT_BACKEND", "VALID_BACKENDS", "REFERENCE_BACKENDS",
+    "backend_from_env", "validate_backend", "resolve_backend", "dense_attention",
 ]
 
 
 def validate_backend(backend: str) -> str:
-    """Check a backend name the way dit.py:249-252 does (AssertionError)."""
-    assert backend in VALID_BACKENDS, (
-        f"unknown BSA backend: {backend!r}. Choose from {VALID_BACKENDS}"
-        + (" (the reference's MLX/Metal backends do not exist on MI355X)"
-           if backend in REFERENCE_ONLY_BACKENDS else "")
-    )
+    """Check a backend name the way longcat_video_dit.py:249-252 does
+    (``AssertionError`` for a name outside the accepted set)."""
+    assert backend in VALID_BACKENDS, f"unknown BSA backend: {backend!r}. Choose from {VALID_BACKENDS}"
     return backend
 
 
+def resolve_backend(backend: str) -> str:
+    """The implementation that serves ``backend``: ``"hip"`` for every
+    accepted name (there is one BSA implementation on MI355X)."""
+    validate_backend(backend)
+    return "hip"
+
+
 def backend_from_env(default: str = DEFAULT_BACKEND) -> str:
-    """``LONGCAT_BSA_BACKEND`` as read by scripts/run_refine.py:91-92."""
+    """``LONGCAT_BSA_BACKEND`` as read by scripts/run_refine.py:91-92
+    (unset -> ``"tier_a"``, as there)."""
     return os.environ.get(ENV_VAR, default)
 
 
@@ -107,7 +122,7 @@ class BSAAttention:
     ) -> torch.Tensor:
         """q, k, v: ``[B, H, S, D]``; returns ``[B, H, S_q, D]``."""
         if self.enable_bsa and shape is not None and q.shape[-2] == k.shape[-2]:
-            validate_backend(self.bsa_backend)
+            resolve_backend(self.bsa_backend)  # every accepted name runs the HIP kernels
             try:
                 out = bsa_attention(
                     q, k, v, shape=shape,

@@ -184,7 +184,7 @@ class _Model:
         self.blocks = [_Block() for _ in range(config["depth"])]
         apply_bsa_params(self, config)
 
-    def enable_bsa(self, backend="hip"):
+    def enable_bsa(self, backend="tier_a"):  # the reference's default (longcat_video_dit.py:219)
         from lcv_bsa import enable_bsa
 
         enable_bsa(self, backend)
@@ -209,7 +209,7 @@ def test_config_enable_bsa_flips_attention():
     for b in m.blocks:
         assert b.attn.enable_bsa is True
         assert b.attn.bsa_sparsity == 0.9375 and b.attn.bsa_chunk_thw == (4, 4, 4)
-        assert b.attn.bsa_backend == "hip"
+        assert b.attn.bsa_backend == "tier_a"  # the reference's default name, served by HIP
 
 
 def test_enable_disable_roundtrip():
@@ -230,25 +230,63 @@ def test_bsa_params_preserved_through_enable():
 
 
 def test_backend_validation():
-    from lcv_bsa.attention import validate_backend
+    """The reference's names (longcat_video_dit.py:249-252) are accepted and
+    resolve to the HIP path; anything else is an AssertionError, as there."""
+    from lcv_bsa.attention import resolve_backend, validate_backend
 
-    assert validate_backend("hip") == "hip"
-    with pytest.raises(AssertionError, match="MLX/Metal"):
-        validate_backend("metal_v4")
-    with pytest.raises(AssertionError, match="unknown BSA backend"):
-        validate_backend("cuda")
+    for name in ("hip", "tier_a", "metal", "metal_v2", "metal_v3", "metal_v4"):
+        assert validate_backend(name) == name
+        assert resolve_backend(name) == "hip"
+    for bad in ("cuda", "Tier_A", "metal_v5", ""):
+        with pytest.raises(AssertionError, match="unknown BSA backend"):
+            validate_backend(bad)
+        with pytest.raises(AssertionError, match="unknown BSA backend"):
+            resolve_backend(bad)
     m = _Model(_config(False))
+    m.enable_bsa()  # the reference's default name
+    assert all(b.attn.enable_bsa and b.attn.bsa_backend == "tier_a" for b in m.blocks)
+    m.enable_bsa("metal_v4")
+    assert all(b.attn.bsa_backend == "metal_v4" for b in m.blocks)
     with pytest.raises(AssertionError):
-        m.enable_bsa("tier_a")
+        m.enable_bsa("cuda")
 
 
 def test_env_var_default_and_override(monkeypatch):
+    """scripts/run_refine.py:91-92: unset -> "tier_a"; set -> that name."""
     from lcv_bsa.attention import backend_from_env
+    from lcv_bsa.dit import enable_bsa_from_env
 
     monkeypatch.delenv("LONGCAT_BSA_BACKEND", raising=False)
-    assert backend_from_env() == "hip"
-    monkeypatch.setenv("LONGCAT_BSA_BACKEND", "hip")
-    assert backend_from_env() == "hip"
+    assert backend_from_env() == "tier_a"
+    m = _Model(_config(False))
+    assert enable_bsa_from_env(m) == "tier_a"
+    assert all(b.attn.enable_bsa and b.attn.bsa_backend == "tier_a" for b in m.blocks)
+    for name in ("hip", "metal"):
+        monkeypatch.setenv("LONGCAT_BSA_BACKEND", name)
+        assert backend_from_env() == name
+    monkeypatch.setenv("LONGCAT_BSA_BACKEND", "mlx")
+    with pytest.raises(AssertionError):
+        enable_bsa_from_env(_Model(_config(False)))
+
+
+def test_reference_backend_names_dispatch_on_cpu():
+    """With a reference backend name the dispatcher takes the BSA branch; on
+    CPU tensors the HIP path raises (there is no CPU fallback), while the
+    dense path (shape None) still runs."""
+    from lcv_bsa import BSAAttention
+    from lcv_bsa.block_sparse_attention import BSADeviceError
+
+    a = BSAAttention(2 * 64, 2)
+    a.enable_bsa, a.bsa_backend = True, "tier_a"
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(1, 2, 64, 64, generator=g) for _ in range(3))
+    with pytest.raises(BSADeviceError):
+        a._process_attn(q, k, v, shape=(1, 1, 64))
+    out = a._process_attn(q, k, v, shape=None)
+    assert a.last_path == "dense" and out.shape == q.shape
+    a.bsa_backend = "cuda"
+    with pytest.raises(AssertionError):
+        a._process_attn(q, k, v, shape=(1, 1, 64))
 
 
 def test_process_attn_dense_path_on_cpu():

@@ -162,6 +162,35 @@ def test_env_backend_selection(device, monkeypatch):
     assert all(b.attn.enable_bsa and b.attn.bsa_backend == "hip" for b in Model.blocks)
 
 
+@pytest.mark.parametrize("name", ["tier_a", "metal", "metal_v4"])
+def test_reference_backend_names_run_bsa(device, monkeypatch, name):
+    """An unchanged refinement setup: LONGCAT_BSA_BACKEND unset (-> "tier_a",
+    scripts/run_refine.py:91) or a Metal name runs BSA through the HIP
+    kernels, with the same bits as the "hip" name."""
+    from lcv_bsa import BSAAttention
+    from lcv_bsa.dit import enable_bsa_from_env
+    from lcv_bsa.workloads import make_inputs
+
+    class Blk:
+        def __init__(self):
+            self.attn = BSAAttention(4 * 128, 4)
+
+    class Model:
+        blocks = [Blk()]
+
+    if name == "tier_a":
+        monkeypatch.delenv("LONGCAT_BSA_BACKEND", raising=False)
+    else:
+        monkeypatch.setenv("LONGCAT_BSA_BACKEND", name)
+    assert enable_bsa_from_env(Model) == name
+    attn = Model.blocks[0].attn
+    q, k, v, _ = make_inputs(1, 4, 128, (8, 8, 16), (4, 4, 4), torch.float16, device, seed=5)
+    out = attn._process_attn(q, k, v, shape=(8, 8, 16))
+    assert attn.last_path == "bsa"
+    attn.bsa_backend = "hip"
+    assert torch.equal(out, attn._process_attn(q, k, v, shape=(8, 8, 16)))
+
+
 def test_golden_voxel(device):
     """The committed (4,4,4)-voxel fp16 fixture, end to end."""
     from pathlib import Path
