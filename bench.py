@@ -57,11 +57,23 @@ def cpu_baseline(w, budget_s: float):
 
     from oracle import bsa_oracle as O
 
+    host_cpus = os.cpu_count() or 1
     try:
-        from threadpoolctl import threadpool_info
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):  # pragma: no cover - non-Linux
+        avail = host_cpus
+    # Every core this process may run on, within the per-GPU CPU share the
+    # job's launcher sets through OMP_NUM_THREADS (a shared host's other
+    # GPUs' jobs keep theirs).
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(avail, share) if share > 0 else avail
+    limiter = None
+    try:
+        from threadpoolctl import threadpool_info, threadpool_limits
+        limiter = threadpool_limits(limits=threads, user_api="blas")
         threads = max(int(i.get("num_threads", 1)) for i in threadpool_info() if i.get("user_api") == "blas")
     except Exception:  # pragma: no cover - threadpoolctl is optional
-        threads = os.cpu_count() or 1
+        pass
     B, H, S, D = w.q.shape
     nb = S // 64
     k = w.top_k
@@ -90,6 +102,8 @@ def cpu_baseline(w, budget_s: float):
                 break
         if t_total >= budget_s:
             break
+    if limiter is not None:
+        limiter.restore_original_limits()
     flops = O.executed_flops(1, 1, done_blocks, k, D)
     cpu = platform.processor() or platform.machine()
     try:
@@ -104,9 +118,14 @@ def cpu_baseline(w, budget_s: float):
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle fp32 (NumPy/OpenBLAS, {threads} threads, {cpu}): pool+route of {heads} "
-                   f"head(s) and sparse attention of {done_blocks} q-blocks x {k} KV blocks in "
-                   f"{t_total:.1f} s; full-workload estimate {t_total * (B * H * nb) / max(done_blocks, 1):.0f} s"),
+        "host_cpus": host_cpus,
+        "available_cpus": avail,
+        "cpu_model": cpu,
+        "sample": (f"oracle fp32 (NumPy/OpenBLAS) on {threads} threads = every CPU available to the "
+                   f"process ({avail} of the host's {host_cpus}, {cpu}) within the per-GPU share "
+                   f"OMP_NUM_THREADS={share or 'unset'}: pool+route of {heads} head(s) and sparse "
+                   f"attention of {done_blocks} q-blocks x {k} KV blocks in {t_total:.1f} s; "
+                   f"full-workload estimate {t_total * (B * H * nb) / max(done_blocks, 1):.0f} s"),
     }
 
 
@@ -198,11 +217,11 @@ def bench_prepare(lib, w, dev, stream, steps: int, warmup: int, seed: int):
     }
 
 
-def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int):
+def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int, dtype=None):
     """One LongCat DiT block at 720p (longcat_video_dit.py:36-138): hidden
     4096, 32 heads of 128, SwiGLU inner 11008, AdaLN from a 512-wide timestep
-    embedding per frame, 512 text tokens, latent grid 16 x 45 x 80, bf16,
-    random weights.  The self-attention runs the fused pre-BSA pass and BSA
+    embedding per frame, 512 text tokens, latent grid 16 x 45 x 80, fp16
+    activations (or ``dtype``), random weights.  The self-attention runs the fused pre-BSA pass and BSA
     (64-token blocks, top-k ``top_k``); the linear layers are torch GEMMs.
 
     A first timed region runs whole blocks; a second attributes time to the
@@ -212,10 +231,11 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int)
 
     from lcv_bsa.dit_block import LongCatSingleStreamBlock
 
+    dt = torch.float16 if dtype is None else dtype
     grid, C, H, L, t_dim = (16, 45, 80), 4096, 32, 512, 512
     N = grid[0] * grid[1] * grid[2]
     torch.manual_seed(seed + 2)
-    blk = LongCatSingleStreamBlock(C, H, 4, t_dim, dtype=torch.bfloat16, device=dev)
+    blk = LongCatSingleStreamBlock(C, H, 4, t_dim, dtype=dt, device=dev)
     with torch.no_grad():
         for name, p in blk.named_parameters():
             if name.endswith("norm.weight") or name == "pre_crs_attn_norm.weight":
@@ -224,8 +244,8 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int)
                 p.normal_(0.0, 0.02)
     blk.attn.enable_bsa, blk.attn.bsa_shape_policy, blk.attn.bsa_top_k = True, "auto", top_k
     gen = torch.Generator(device=dev).manual_seed(seed + 3)
-    x = torch.randn((1, N, C), generator=gen, device=dev).to(torch.bfloat16)
-    y = torch.randn((1, L, C), generator=gen, device=dev).to(torch.bfloat16)
+    x = torch.randn((1, N, C), generator=gen, device=dev).to(dt)
+    y = torch.randn((1, L, C), generator=gen, device=dev).to(dt)
     t = torch.randn((1, grid[0], t_dim), generator=gen, device=dev)
 
     def step():
@@ -278,10 +298,11 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int)
     other = ms_instr - per["self_attn"] - per["cross_attn"] - per["pre_cross_norm"] - ffn_ms
     del blk, x, y, t
     torch.cuda.empty_cache()
+    name = DTYPE_NAME[str(dt).split(".")[1]]
     return {
         "workload": "one LongCat-Video DiT block, 720p refinement latents (16, 45, 80) = 57600 tokens, hidden 4096, "
-                    "32 heads x 128, SwiGLU 11008, 512 text tokens, bf16, random weights",
-        "dtype": "bf16",
+                    f"32 heads x 128, SwiGLU 11008, 512 text tokens, {name} activations, random weights",
+        "dtype": name,
         "bsa": f"fused prepare_qk + BSA, 64-token blocks, top-k {top_k} of 900",
         "ms": round(ms, 3),
         "bsa_ms": round(bsa_ms, 3),
@@ -325,7 +346,7 @@ def bench_kv_split(lib, dev, stream, steps: int, warmup: int, seed: int):
     q = q_all[:, :, nc:]
     qshape, kshape, chunk = (1, 1, Sq), (1, 1, Sk), (1, 1, 64)
     idx = select_block_indices(mean_pool_blocks_3d(q, qshape, chunk), mean_pool_blocks_3d(k, kshape, chunk), top_k)
-    order = schedule_block_order(idx)
+    order = schedule_block_order(idx, Sk // 64)
     out = torch.empty_like(q)
     sh = stream.cuda_stream
     scale = 1.0 / math.sqrt(D)
@@ -626,10 +647,11 @@ def main() -> int:
         log(f"geometry at (16,48,80): voxel {vp['voxel_4x4x4']['ms_attention']:.3f} ms, "
             f"contiguous {vp['contiguous_64']['ms_attention']:.3f} ms")
     if args.config == "c2" and not args.no_dit_block:
-        blk = bench_dit_block(dev, stream, max(3, args.steps // 2), 2, args.seed, top_k)
-        result["dit_block"] = blk
-        log(f"DiT block 720p bf16: {blk['ms']:.2f} ms, BSA {blk['bsa_ms']:.2f} ms = "
-            f"{100 * blk['bsa_share']:.1f} % ({blk['breakdown_ms']})")
+        for key, dt in (("dit_block", torch.float16), ("dit_block_bf16", torch.bfloat16)):
+            blk = bench_dit_block(dev, stream, max(3, args.steps // 2), 2, args.seed, top_k, dt)
+            result[key] = blk
+            log(f"DiT block 720p {blk['dtype']}: {blk['ms']:.2f} ms, BSA {blk['bsa_ms']:.2f} ms = "
+                f"{100 * blk['bsa_share']:.1f} % ({blk['breakdown_ms']})")
     if not args.no_cpu_baseline:
         t0 = time.time()
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_budget)

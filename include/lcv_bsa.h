@@ -121,6 +121,16 @@ int lcv_bsa_schedule(const int32_t* idx, int64_t B, int64_t H, int64_t nq,
                      int64_t top_k, int32_t* order, void* stream);
 
 /*
+ * lcv_bsa_schedule for routing lists over nk K/V blocks (S_q != S_k, the
+ * input of lcv_bsa_attn_fwd_kv): list entries are K/V block ids in [0, nk)
+ * and sort by their value up to nk (lcv_bsa_schedule is this with nk = nq).
+ * nq <= 4096, nk < 2^20.  No counterpart in the reference, whose layer sends
+ * S_q != S_k to dense attention (attention.py:89, 218-221, 273).
+ */
+int lcv_bsa_schedule_kv(const int32_t* idx, int64_t B, int64_t H, int64_t nq,
+                        int64_t nk, int64_t top_k, int32_t* order, void* stream);
+
+/*
  * Sparse attention over given block lists (the kernel-level entry):
  *   out[b,h,s,:] = softmax_j(sm_scale * q[s].k[j]) v[j]
  * over every key j in the blocks idx[b,h,block_of(s),0..top_k-1].

@@ -237,8 +237,18 @@ struct MfmaCfg {
   __device__ static int vswz(int r) { return 4 * ((r / RP) % (DC / 4)); }
 };
 
+// Waves per SIMD the register allocation must allow.  D = 128 uses the
+// 256-register budget of two waves.  D = 64 holds three (132 registers; its
+// 16 KB of LDS per workgroup would allow eight workgroups per CU): asking
+// for four makes the allocator spill to scratch.
+template <int D>
+struct MfmaOccupancy {
+  static constexpr int kWaves = D == 128 ? 2 : 3;
+};
+
 template <typename T, int D>
-__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(128)
+__attribute__((amdgpu_waves_per_eu(MfmaOccupancy<D>::kWaves, MfmaOccupancy<D>::kWaves)))
 void attn_mfma_kernel(AttnParams p) {
   typedef MfmaCfg<T, D> C;
   typedef typename Mfma<T>::vec8 vec8;

@@ -197,10 +197,11 @@ hipError_t launch_attn(const AttnParams& p, int dtype, int D, hipStream_t stream
 bool attn_supported(int dtype, int D);
 bool attn_uses_mfma(int dtype, int D);
 
-// Per-head q-block launch order from the routing lists (nq <= 4096).
-hipError_t launch_schedule(const int32_t* idx, int BH, int nq, int top_k, int32_t* order,
+// Per-head q-block launch order from the routing lists (nq <= 4096 q-blocks,
+// entries are K/V block ids in [0, nk)).
+hipError_t launch_schedule(const int32_t* idx, int BH, int nq, int nk, int top_k, int32_t* order,
                            hipStream_t stream);
-bool schedule_supported(int nq);
+bool schedule_supported(int nq, int nk);
 
 // Fused RMSNorm + 3D RoPE + block means of q and k (fp16/bf16, D 64/128).
 // The RoPE table holds cos and sin per axis: [rT*dt/2 | rT*dt/2 | rH*dh/2 |

@@ -256,13 +256,21 @@ int lcv_bsa_select(const float* qbar, const float* kbar, int64_t B, int64_t H, i
 
 int lcv_bsa_schedule(const int32_t* idx, int64_t B, int64_t H, int64_t nq, int64_t top_k,
                      int32_t* order, void* stream) {
+  return lcv_bsa_schedule_kv(idx, B, H, nq, nq, top_k, order, stream);
+}
+
+int lcv_bsa_schedule_kv(const int32_t* idx, int64_t B, int64_t H, int64_t nq, int64_t nk,
+                        int64_t top_k, int32_t* order, void* stream) {
   if (!idx || !order) return fail(LCV_BSA_ERR_INVALID_ARG, "null pointer");
-  if (B <= 0 || H <= 0 || nq <= 0 || top_k <= 0)
-    return fail(LCV_BSA_ERR_INVALID_ARG, "B, H, nq, top_k must be positive");
-  if (!lcv::schedule_supported((int)std::min<int64_t>(nq, kI32Max)) || B * H > kI32Max ||
-      B * H * nq * top_k > ((int64_t)1 << 40))
-    return fail(LCV_BSA_ERR_UNSUPPORTED, "scheduling supports nq <= 4096 (got %lld)", (long long)nq);
-  return launch_status(lcv::launch_schedule(idx, (int)(B * H), (int)nq, (int)top_k, order,
+  if (B <= 0 || H <= 0 || nq <= 0 || nk <= 0 || top_k <= 0)
+    return fail(LCV_BSA_ERR_INVALID_ARG, "B, H, nq, nk, top_k must be positive");
+  if (!lcv::schedule_supported((int)std::min<int64_t>(nq, kI32Max),
+                               (int)std::min<int64_t>(nk, kI32Max)) ||
+      B * H > kI32Max || B * H * nq * top_k > ((int64_t)1 << 40))
+    return fail(LCV_BSA_ERR_UNSUPPORTED,
+                "scheduling supports nq <= 4096 and nk < 2^20 (got nq=%lld, nk=%lld)",
+                (long long)nq, (long long)nk);
+  return launch_status(lcv::launch_schedule(idx, (int)(B * H), (int)nq, (int)nk, (int)top_k, order,
                                             (hipStream_t)stream),
                        "lcv_bsa_schedule");
 }
@@ -351,9 +359,9 @@ int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype, int6
   st = launch_status(lcv::launch_topk(score, (int)B, (int)H, (int)nb, (int)nb, (int)top_k, idx, s),
                      "lcv_bsa_forward(top-k)");
   if (st) return st;
-  const bool sched = lcv::schedule_supported((int)nb);
+  const bool sched = lcv::schedule_supported((int)nb, (int)nb);
   if (sched) {
-    st = launch_status(lcv::launch_schedule(idx, (int)(B * H), (int)nb, (int)top_k, order, s),
+    st = launch_status(lcv::launch_schedule(idx, (int)(B * H), (int)nb, (int)nb, (int)top_k, order, s),
                        "lcv_bsa_forward(schedule)");
     if (st) return st;
   }

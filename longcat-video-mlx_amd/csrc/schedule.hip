@@ -9,9 +9,10 @@
 // work ids land on the same XCD (xcd_linear_work_id), so the sorted runs
 // execute together.
 //
-// q-block i's key is (first, median, i), entries outside [0, nq) counting as
-// nq.  The key is unique, so the sorted order is a permutation, the same one
-// any correct sort gives.  Two sorts:
+// q-block i's key is (first, median, i), with entries outside [0, nk) (the
+// K/V block count of the head, which exceeds nq when keys outnumber queries)
+// counting as nk.  The key is unique, so the sorted order is a permutation,
+// the same one any correct sort gives.  Two sorts:
 //   * nq <= 1024: one workgroup per head, one key per thread, bitonic; the
 //     stages whose partner lies in the same wave exchange keys with lane
 //     shuffles, the rest through LDS;
@@ -26,21 +27,26 @@ namespace lcv {
 namespace {
 
 constexpr int kMaxSched = 4096;
+constexpr int kMaxKvBlocks = (1 << 20) - 1;  // a 20-bit key field holds 0 .. nk
 constexpr int kRankThreads = 256;
 
+// Sort key of q-block i: 20 bits each of its first and median list entries
+// (out-of-range entries clamped to nk <= kMaxKvBlocks) and of i.
+__device__ __forceinline__ uint64_t order_key(const int32_t* rows, int i, int nk, int top_k) {
+  int first = rows[(int64_t)i * top_k];
+  int median = rows[(int64_t)i * top_k + top_k / 2];
+  first = (first < 0 || first >= nk) ? nk : first;
+  median = (median < 0 || median >= nk) ? nk : median;
+  return ((uint64_t)first << 40) | ((uint64_t)median << 20) | (uint64_t)i;
+}
+
 __global__ __launch_bounds__(kRankThreads) void schedule_rank_kernel(const int32_t* idx, int nq,
-                                                                     int top_k, int32_t* order) {
+                                                                     int nk, int top_k,
+                                                                     int32_t* order) {
   __shared__ uint64_t keys[kMaxSched];
   const int bh = blockIdx.x;
   const int32_t* rows = idx + (int64_t)bh * nq * top_k;
-  const int mid = top_k / 2;
-  for (int i = threadIdx.x; i < nq; i += kRankThreads) {
-    int first = rows[(int64_t)i * top_k];
-    int median = rows[(int64_t)i * top_k + mid];
-    first = (first < 0 || first >= nq) ? nq : first;
-    median = (median < 0 || median >= nq) ? nq : median;
-    keys[i] = ((uint64_t)first << 40) | ((uint64_t)median << 20) | (uint64_t)i;
-  }
+  for (int i = threadIdx.x; i < nq; i += kRankThreads) keys[i] = order_key(rows, i, nk, top_k);
   __syncthreads();
   const int i = blockIdx.y * kRankThreads + threadIdx.x;
   if (i >= nq) return;
@@ -63,20 +69,13 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int m) {
 }
 
 __global__ __launch_bounds__(kSmallSched) void schedule_small_kernel(const int32_t* idx, int nq,
-                                                                     int top_k, int32_t* order) {
+                                                                     int nk, int top_k,
+                                                                     int32_t* order) {
   __shared__ uint64_t xch[kSmallSched];
   const int bh = blockIdx.x;
   const int i = threadIdx.x;
   const int32_t* rows = idx + (int64_t)bh * nq * top_k;
-  const int mid = top_k / 2;
-  uint64_t key = ~0ull;  // padding sorts last
-  if (i < nq) {
-    int first = rows[(int64_t)i * top_k];
-    int median = rows[(int64_t)i * top_k + mid];
-    first = (first < 0 || first >= nq) ? nq : first;
-    median = (median < 0 || median >= nq) ? nq : median;
-    key = ((uint64_t)first << 40) | ((uint64_t)median << 20) | (uint64_t)i;
-  }
+  uint64_t key = i < nq ? order_key(rows, i, nk, top_k) : ~0ull;  // padding sorts last
   for (int k = 2; k <= kSmallSched; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
       uint64_t other;
@@ -100,18 +99,20 @@ __global__ __launch_bounds__(kSmallSched) void schedule_small_kernel(const int32
 
 }  // namespace
 
-bool schedule_supported(int nq) { return nq >= 1 && nq <= kMaxSched; }
+bool schedule_supported(int nq, int nk) {
+  return nq >= 1 && nq <= kMaxSched && nk >= 1 && nk <= kMaxKvBlocks;
+}
 
-hipError_t launch_schedule(const int32_t* idx, int BH, int nq, int top_k, int32_t* order,
+hipError_t launch_schedule(const int32_t* idx, int BH, int nq, int nk, int top_k, int32_t* order,
                            hipStream_t stream) {
-  if (!schedule_supported(nq) || BH < 1 || top_k < 1) return hipErrorInvalidValue;
+  if (!schedule_supported(nq, nk) || BH < 1 || top_k < 1) return hipErrorInvalidValue;
   if (nq <= kSmallSched) {
-    hipLaunchKernelGGL(schedule_small_kernel, dim3(BH), dim3(kSmallSched), 0, stream, idx, nq,
+    hipLaunchKernelGGL(schedule_small_kernel, dim3(BH), dim3(kSmallSched), 0, stream, idx, nq, nk,
                        top_k, order);
     return hipGetLastError();
   }
   const dim3 grid((unsigned)BH, (unsigned)((nq + kRankThreads - 1) / kRankThreads));
-  hipLaunchKernelGGL(schedule_rank_kernel, grid, dim3(kRankThreads), 0, stream, idx, nq, top_k,
+  hipLaunchKernelGGL(schedule_rank_kernel, grid, dim3(kRankThreads), 0, stream, idx, nq, nk, top_k,
                      order);
   return hipGetLastError();
 }

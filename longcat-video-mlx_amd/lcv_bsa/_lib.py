@@ -58,6 +58,8 @@ _SIGNATURES = {
                                c_int64, c_void_p, c_void_p]),
     "lcv_bsa_schedule": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p,
                                  c_void_p]),
+    "lcv_bsa_schedule_kv": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                    c_void_p, c_void_p]),
     "lcv_bsa_attn_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
                                  c_int64, Strides, Strides, Strides, c_void_p, c_void_p, c_int64,
                                  c_float, Geom, c_void_p, Strides, c_void_p]),

@@ -31,19 +31,21 @@ __all__ = [
 MAX_SCHEDULED_BLOCKS = 4096
 
 
-def schedule_block_order(block_indices: torch.Tensor) -> torch.Tensor:
+def schedule_block_order(block_indices: torch.Tensor, num_kv_blocks: Optional[int] = None) -> torch.Tensor:
     """Per-head launch order of the q-blocks (``[B, H, nq]`` int32 permutation).
 
     q-blocks are sorted by the first and middle entries of their routing
     lists, so that blocks whose ascending lists start together run together
     and re-use each other's K/V tiles from L2.  Any order gives the same
-    attention output.  nq <= 4096.
+    attention output.  ``num_kv_blocks`` is the K/V block count the entries
+    index (default: nq, the S_q == S_k case).  nq <= 4096.
     """
     _require_device(block_indices)
     bi = block_indices.to(torch.int32).contiguous()
     B, H, nq, k = bi.shape
+    nk = nq if num_kv_blocks is None else int(num_kv_blocks)
     order = torch.empty((B, H, nq), dtype=torch.int32, device=bi.device)
-    st = _lib.load().lcv_bsa_schedule(bi.data_ptr(), B, H, nq, k, order.data_ptr(), _stream(bi))
+    st = _lib.load().lcv_bsa_schedule_kv(bi.data_ptr(), B, H, nq, nk, k, order.data_ptr(), _stream(bi))
     _lib.check(st, "schedule_block_order")
     return order
 
@@ -122,7 +124,8 @@ def bsa_attention_hip(
     code = _dtype_code(q)
     if code != _lib.F32:
         q, k, v = _aligned_rows(q), _aligned_rows(k), _aligned_rows(v)
-    order = schedule_block_order(bi) if nb <= MAX_SCHEDULED_BLOCKS else None
+    nk = num_blocks(kshape, chunk_thw)
+    order = schedule_block_order(bi, nk) if nb <= MAX_SCHEDULED_BLOCKS else None
     out = _output(out, q)
     st = _lib.load().lcv_bsa_attn_fwd_kv(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), code, B, H, S, Sk, D,

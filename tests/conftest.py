@@ -47,3 +47,30 @@ def assert_close_report(actual, expected, max_abs: float, mean_abs: float, what:
     assert mx <= max_abs and mn <= mean_abs, (
         f"{what}: max_abs={mx:.3e} (tol {max_abs:.1e}) mean_abs={mn:.3e} (tol {mean_abs:.1e})")
     return mx, mn
+
+
+def gathered_attention_fp32(q, k, v, idx, scale, step=128):
+    """fp32 attention of every q-block over its listed 64-token K/V blocks of
+    contiguous-run geometry (shape (1, 1, S), chunk (1, 1, 64)), in torch on
+    q's device: gather, fp32 scores, softmax, fp32 P V.  Shares no code with
+    the HIP kernels; pinned against the NumPy oracle by
+    test_cpu_host.py::test_gathered_reference_matches_oracle."""
+    import torch
+
+    B, H, S, D = q.shape
+    nb, top_k = S // 64, idx.shape[-1]
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    for b in range(B):
+        for h in range(H):
+            qh = q[b, h].float().reshape(nb, 64, D)
+            kh = k[b, h].float().reshape(-1, 64, D)
+            vh = v[b, h].float().reshape(-1, 64, D)
+            ih = idx[b, h].long()
+            for n0 in range(0, nb, step):
+                n = min(step, nb - n0)
+                ii = ih[n0:n0 + n]
+                kt = kh[ii].reshape(n, top_k * 64, D).transpose(1, 2).contiguous()
+                vg = vh[ii].reshape(n, top_k * 64, D).contiguous()
+                p = torch.softmax(torch.bmm(qh[n0:n0 + n].contiguous(), kt) * scale, dim=-1)
+                out[b, h, n0 * 64:(n0 + n) * 64] = torch.bmm(p, vg).reshape(n * 64, D)
+    return out

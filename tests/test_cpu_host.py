@@ -492,3 +492,23 @@ def test_header_compiles_for_c_and_cpp_callers(tmp_path, lang, std):
                         f"-I{REPO / 'include'}", "-fsyntax-only", str(src)],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
+
+
+def test_gathered_reference_matches_oracle():
+    """The fp32 torch reference that the full-size GPU tests compare every
+    q-block with equals the fp64 oracle on a small routed case (unsorted
+    lists included), and a planted key transpose in it is caught."""
+    from conftest import gathered_attention_fp32
+
+    g = torch.Generator().manual_seed(3)
+    B, H, S, D, k = 2, 3, 1024, 32, 5
+    q, kk, v = (torch.randn(B, H, S, D, generator=g) for _ in range(3))
+    nb = S // 64
+    idx = torch.stack([torch.randperm(nb, generator=g)[:k] for _ in range(B * H * nb)]).reshape(B, H, nb, k)
+    idx = idx.to(torch.int32)
+    got = gathered_attention_fp32(q, kk, v, idx, 0.3, step=5).numpy()
+    ref = O.sparse_attention_from_indices(q.numpy(), kk.numpy(), v.numpy(), idx.numpy(), (1, 1, S),
+                                          (1, 1, 64), 0.3)
+    assert np.abs(got - ref).max() < 2e-5
+    wrong = gathered_attention_fp32(q, kk.transpose(2, 3).reshape(B, H, S, D), v, idx, 0.3).numpy()
+    assert np.abs(wrong - ref).max() > 1e-2

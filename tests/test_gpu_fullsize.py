@@ -1,9 +1,15 @@
 """Full refinement shapes on the device (B x 32 heads x S=28800/57600, D=128).
 
+For every top-k of the config -- the headline ceil count (29 at C1, 57 at
+C2, 113 / 57 / 29 at C3) and the reference's floor count one below it:
+
 * routing: every (b, h, q-block) row of the HIP top-k equals the oracle's
-  fp64 selection (ascending sets), for the ceil and the floor top-k;
-* attention: a sample of q-blocks against the fp64 oracle (north-star
-  tolerance for fp16: max-abs 2e-3, mean-abs 2e-4; bf16: 1e-2 / 2e-3);
+  fp64 selection (ascending sets);
+* attention, whole output: every q-block against an fp32 reference computed
+  independently on the GPU with torch (gather the listed K/V blocks, fp32
+  scores, softmax, fp32 P V), at the north-star tolerance (fp16: max-abs
+  2e-3, mean-abs 2e-4; bf16: 1e-2 / 2e-3);
+* attention, sample: 12 q-blocks against the fp64 NumPy oracle;
 * size-independent properties over the whole output: finite, a convex
   combination of V rows (|out| <= max|v| per head), exact determinism, and
   v = 1 maps to 1.
@@ -17,7 +23,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import assert_close_report
+from conftest import assert_close_report, gathered_attention_fp32
 from oracle import bsa_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -53,6 +59,19 @@ def _check_attention_sample(q, k, v, idx, out, dtype, n_samples=12, seed=0):
         ref.append(r[0, 0, n * 64:(n + 1) * 64])
         got.append(out[b, h, n * 64:(n + 1) * 64].float().cpu().numpy())
     assert_close_report(np.stack(got), np.stack(ref), *TOL[dtype], "sampled q-blocks")
+
+
+def _check_whole_output(q, k, v, idx, out, dtype, scale):
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ref = gathered_attention_fp32(q, k, v, idx, scale)
+    d = (out.float() - ref).abs()
+    mx, mn = float(d.max()), float(d.mean())
+    tol_max, tol_mean = TOL[dtype]
+    assert torch.isfinite(out).all()
+    assert mx <= tol_max and mn <= tol_mean, (
+        f"whole output vs fp32 GPU reference: max_abs={mx:.3e} (tol {tol_max:.1e}) "
+        f"mean_abs={mn:.3e} (tol {tol_mean:.1e})")
+    return mx, mn
 
 
 def _properties(q, k, v, idx, out, top_k):
@@ -91,9 +110,14 @@ def _run(dev, name, top_ks, seed=0):
             assert mism == 0, f"{name} k={kk}: {mism} routing rows differ"
             print(f"{name} k={kk}: routing exact over {ref_idx.shape[0] * ref_idx.shape[1] * ref_idx.shape[2]} rows "
                   f"({time.time() - t0:.1f}s)", flush=True)
-        _check_attention_sample(w.q, w.k, w.v, idx, out, w.q.dtype, seed=k)
-        _properties(w.q, w.k, w.v, idx, out, kk)
-        print(f"{name} k={k}: attention sample + properties ok ({time.time() - t0:.1f}s)", flush=True)
+            mx, mn = _check_whole_output(w.q, w.k, w.v, idx, out, w.q.dtype, w.sm_scale)
+            print(f"{name} k={kk}: whole output vs fp32 GPU reference max_abs={mx:.2e} mean_abs={mn:.2e} "
+                  f"({time.time() - t0:.1f}s)", flush=True)
+            _check_attention_sample(w.q, w.k, w.v, idx, out, w.q.dtype, seed=kk)
+            _properties(w.q, w.k, w.v, idx, out, kk)
+            print(f"{name} k={kk}: fp64 sample + properties ok ({time.time() - t0:.1f}s)", flush=True)
+            del out, idx
+            torch.cuda.empty_cache()
     # the reference's own count rule (floor) through the default path
     nb = w.num_blocks
     out = bsa_attention(w.q, w.k, w.v, shape=w.shape, chunk_thw=w.chunk_thw)

@@ -403,6 +403,28 @@ def test_schedule_permutation_sorted_by_key(device, nb, k):
         assert keys == sorted(keys)
 
 
+@pytest.mark.parametrize("nq,nk,k", [(900, 1125, 71), (64, 300, 4), (1100, 2000, 9)])
+def test_schedule_kv_sorts_by_kv_block_ids(device, nq, nk, k):
+    """S_q != S_k routing: entries are K/V block ids up to nk > nq.  Lists
+    that start at or above nq sort by their value (not as padding); only
+    entries outside [0, nk) count as nk."""
+    from lcv_bsa import schedule_block_order
+
+    rng = np.random.default_rng(nq + nk)
+    idx = np.sort(np.stack([rng.choice(nk, size=k, replace=False) for _ in range(2 * nq)]), axis=-1)
+    idx = idx.reshape(1, 2, nq, k).astype(np.int32)
+    idx[0, 1, 5, :] = -1
+    idx[0, 1, 6, 0] = nk  # out of range: sorts as nk
+    assert (idx[..., 0] >= nq).any()
+    order = schedule_block_order(torch.from_numpy(idx).to(device), nk).cpu().numpy()
+    for h in range(2):
+        assert sorted(order[0, h].tolist()) == list(range(nq))
+        first = np.where((idx[0, h, :, 0] >= 0) & (idx[0, h, :, 0] < nk), idx[0, h, :, 0], nk)
+        med = np.where((idx[0, h, :, k // 2] >= 0) & (idx[0, h, :, k // 2] < nk), idx[0, h, :, k // 2], nk)
+        keys = [(first[i], med[i], i) for i in order[0, h]]
+        assert keys == sorted(keys)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_attention_launch_order_changes_only_rounding(device, dtype):
     from lcv_bsa import schedule_block_order

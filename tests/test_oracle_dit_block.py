@@ -239,3 +239,42 @@ def test_kv_cache_continuation_equals_split_noise_branch():
     noise_grid = (full_grid[0] - ncl,) + full_grid[1:]
     cont, _ = DB.self_attention_kv_cache(x[:, nc:], p, noise_grid, H, "bf16", (kc, vc), ncl, dense)
     assert np.array_equal(cont, split[:, nc:])
+
+
+def _block_check(got, ref, dtype_ulp, what):
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    err = np.abs(got.astype(np.float64) - ref)
+    bound = 2 * dtype_ulp * np.abs(ref) + 0.02 * rms
+    assert np.all(err <= bound), f"{what}: max excess {np.max(err / bound):.2f}"
+    assert err.mean() < 0.005 * rms, f"{what}: mean error {err.mean() / rms:.2e} of rms"
+    return float(np.max(err / bound))
+
+
+def test_torch_block_reference_matches_oracle():
+    """The torch fp32 restatement used at 720p on the GPU (tests/block_reference.py)
+    agrees with the NumPy block oracle on a small block in fp16 and bf16,
+    with BSA routed over 64-token runs, and a planted dropped FFN gate is
+    caught."""
+    from block_reference import dit_block_torch
+
+    C, H, t_dim, L, grid, top_k = 128, 2, 32, 16, (4, 4, 16), 2
+    N = int(np.prod(grid))
+    p = _params(C, H, t_dim=t_dim, seed=5)
+    rng = np.random.default_rng(6)
+    for dt, name, ulp in ((torch.float16, "f16", 2.0 ** -11), (torch.bfloat16, "bf16", 2.0 ** -8)):
+        x = O.round_to(rng.normal(size=(1, N, C)).astype(np.float32), name)
+        y = O.round_to(rng.normal(size=(1, L, C)).astype(np.float32), name)
+        t = rng.normal(size=(1, grid[0], t_dim)).astype(np.float32)
+        idx = np.sort(np.stack([rng.choice(N // 64, size=top_k, replace=False)
+                                for _ in range(H * (N // 64))]), -1).reshape(1, H, N // 64, top_k)
+        idx = idx.astype(np.int32)
+        ref, _ = DB.dit_block(x, y, t, p, grid, H, name, {"all": ((1, 1, N), (1, 1, 64)), "top_k": top_k},
+                              block_indices={"all": idx})
+        tp = {k: torch.from_numpy(v) for k, v in p.items()}
+        args = (torch.from_numpy(x).to(dt), torch.from_numpy(y).to(dt), torch.from_numpy(t))
+        got = dit_block_torch(*args, tp, grid, H, dt, torch.from_numpy(idx)).numpy()
+        _block_check(got, ref, ulp, f"torch block reference {name}")
+        tp_bad = dict(tp)
+        tp_bad["ffn.w2.weight"] = torch.zeros_like(tp["ffn.w2.weight"])
+        bad = dit_block_torch(*args, tp_bad, grid, H, dt, torch.from_numpy(idx)).numpy()
+        assert np.abs(bad - ref).max() > 0.1
