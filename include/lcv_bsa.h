@@ -244,6 +244,33 @@ int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype,
                     int32_t* idx, void* out, lcv_bsa_strides os,
                     void* stream);
 
+/* Bytes of device scratch lcv_bsa_forward_noalloc holds per GPU. */
+#define LCV_BSA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/*
+ * lcv_bsa_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).  No counterpart in the
+ * reference.  Same arguments and result as lcv_bsa_forward (routing by the
+ * fused select kernel, which keeps block scores on chip; the routing is the
+ * same as the scores + top-k route).  The pooled means and the launch order
+ * live in a fixed device array of LCV_BSA_NOALLOC_SCRATCH_BYTES that every
+ * GPU the library runs on holds until the process ends:
+ *   2 * round256(B*H*nb*D*4) + round256(B*H*nb*4) <= 64 MiB
+ * (B*H*nb <= 65,280 at D = 128: both 720p configurations fit); larger
+ * problems get LCV_BSA_ERR_UNSUPPORTED before any device work.  The call
+ * allocates and frees nothing.  Calls on one GPU share its array: calls
+ * that overlap in time on one GPU (other streams, other threads) race and
+ * must be serialised by the caller.  Nothing in the array carries over from
+ * one call to the next (each call writes every byte it reads).
+ */
+int lcv_bsa_forward_noalloc(const void* q, const void* k, const void* v,
+                            int dtype, int64_t B, int64_t H, int64_t S,
+                            int64_t D, lcv_bsa_strides qs, lcv_bsa_strides ks,
+                            lcv_bsa_strides vs, int64_t top_k, float sm_scale,
+                            lcv_bsa_geom g, int32_t* idx, void* out,
+                            lcv_bsa_strides os, void* stream);
+
 /*
  * Token -> block map: out[s] = block of token s (int32, length T*Hl*Wl).
  * Replaces build_token_block_indices, block_sparse_attention.py:137-159.

@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "bsa_common.h"
 
@@ -300,6 +301,8 @@ int lcv_bsa_attn_fwd_kv(const void* q, const void* k, const void* v, int dtype, 
                        "lcv_bsa_attn_fwd");
 }
 
+}  // extern "C"
+
 namespace {
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 size_t pooled_bytes(int64_t B, int64_t H, int64_t nb, int64_t D) {
@@ -310,65 +313,178 @@ size_t score_bytes(int64_t B, int64_t H, int64_t nb) {
 }
 }  // namespace
 
+extern "C" {
+
 size_t lcv_bsa_forward_workspace_bytes(int64_t B, int64_t H, int64_t nb, int64_t D) {
   if (B <= 0 || H <= 0 || nb <= 0 || D <= 0) return 0;
   return 2 * pooled_bytes(B, H, nb, D) + score_bytes(B, H, nb) +
          align256((size_t)B * H * nb * sizeof(int32_t));
 }
 
-int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
-                    int64_t S, int64_t D, lcv_bsa_strides qs, lcv_bsa_strides ks,
-                    lcv_bsa_strides vs, int64_t top_k, float sm_scale, lcv_bsa_geom g,
-                    void* workspace, size_t workspace_bytes, int32_t* idx, void* out,
-                    lcv_bsa_strides os, void* stream) {
-  int64_t nb = 0, nk = 0, bs = 0;
+}  // extern "C"
+
+namespace {
+
+// Validation shared by both forward entry points; fills nb and bs.
+int check_forward_args(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                       int64_t H, int64_t S, int64_t D, const lcv_bsa_strides& qs,
+                       const lcv_bsa_strides& ks, const lcv_bsa_strides& vs, int64_t top_k,
+                       float sm_scale, const lcv_bsa_geom& g, const int32_t* idx, const void* out,
+                       const lcv_bsa_strides& os, int64_t* nb, int64_t* bs) {
+  int64_t nk = 0;
   int st = check_attn_args(q, k, v, out, dtype, B, H, S, S, D, qs, ks, vs, os, top_k, sm_scale, g,
-                           g, &nb, &nk, &bs);
+                           g, nb, &nk, bs);
   if (st) return st;
-  if (!idx || !workspace) return fail(LCV_BSA_ERR_INVALID_ARG, "null idx or workspace pointer");
-  if (top_k > nb)
+  if (!idx) return fail(LCV_BSA_ERR_INVALID_ARG, "null idx pointer");
+  if (top_k > *nb)
     return fail(LCV_BSA_ERR_INVALID_ARG, "top_k=%lld exceeds num_blocks=%lld", (long long)top_k,
-                (long long)nb);
-  if ((st = check_route(B, H, nb, nb, D, true))) return st;
-  const size_t need = lcv_bsa_forward_workspace_bytes(B, H, nb, D);
-  if (workspace_bytes < need || ((uintptr_t)workspace & 255u))
-    return fail(LCV_BSA_ERR_INVALID_ARG,
-                "workspace must be 256-byte aligned and hold %zu bytes (got %zu)", need,
-                workspace_bytes);
-  hipStream_t s = (hipStream_t)stream;
-  const size_t pb = pooled_bytes(B, H, nb, D);
-  char* ws = reinterpret_cast<char*>(workspace);
-  float* qbar = reinterpret_cast<float*>(ws);
-  float* kbar = reinterpret_cast<float*>(ws + pb);
-  float* score = reinterpret_cast<float*>(ws + 2 * pb);
-  int32_t* order = reinterpret_cast<int32_t*>(ws + 2 * pb + score_bytes(B, H, nb));
+                (long long)*nb);
+  return check_route(B, H, *nb, *nb, D, true);
+}
+
+// pool -> routing -> schedule -> attention on validated arguments.  With a
+// score buffer the routing runs as the score GEMM (each staged key chunk
+// shared by 64 rows) plus the per-row top-k; without one, as the fused
+// select kernel that keeps the scores on chip.  Both give the same routing.
+int run_forward(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                int64_t S, int64_t D, const lcv_bsa_strides& qs, const lcv_bsa_strides& ks,
+                const lcv_bsa_strides& vs, int64_t top_k, float sm_scale, const lcv_bsa_geom& g,
+                int64_t nb, int64_t bs, float* qbar, float* kbar, float* score, int32_t* order,
+                int32_t* idx, void* out, const lcv_bsa_strides& os, hipStream_t s,
+                const char* name) {
+  char what[96];
   const lcv::Tensor4 ts[2] = {{q, qs.b, qs.h, qs.s}, {k, ks.b, ks.h, ks.s}};
   float* outs[2] = {qbar, kbar};
   const lcv::Geom gg = lcv::make_geom(g);
-  st = launch_status(lcv::launch_pool(ts, 2, dtype, (int)B, (int)H, (int)D, (int)nb, (int)bs, gg,
-                                      outs, s),
-                     "lcv_bsa_forward(pool)");
+  snprintf(what, sizeof(what), "%s(pool)", name);
+  int st = launch_status(lcv::launch_pool(ts, 2, dtype, (int)B, (int)H, (int)D, (int)nb, (int)bs,
+                                          gg, outs, s),
+                         what);
   if (st) return st;
-  // Routing in two kernels through the score buffer: the score GEMM with
-  // each staged key chunk shared by 64 rows, then the top-k one row per wave
-  // (together faster than the fused select at 720p sizes; same selection).
-  st = launch_status(lcv::launch_scores(qbar, kbar, (int)B, (int)H, (int)nb, (int)nb, (int)D,
-                                        score, s),
-                     "lcv_bsa_forward(scores)");
-  if (st) return st;
-  st = launch_status(lcv::launch_topk(score, (int)B, (int)H, (int)nb, (int)nb, (int)top_k, idx, s),
-                     "lcv_bsa_forward(top-k)");
+  if (score) {
+    snprintf(what, sizeof(what), "%s(scores)", name);
+    st = launch_status(lcv::launch_scores(qbar, kbar, (int)B, (int)H, (int)nb, (int)nb, (int)D,
+                                          score, s),
+                       what);
+    if (st) return st;
+    snprintf(what, sizeof(what), "%s(top-k)", name);
+    st = launch_status(lcv::launch_topk(score, (int)B, (int)H, (int)nb, (int)nb, (int)top_k, idx,
+                                        s),
+                       what);
+  } else {
+    snprintf(what, sizeof(what), "%s(select)", name);
+    st = launch_status(lcv::launch_select(qbar, kbar, (int)B, (int)H, (int)nb, (int)nb, (int)D,
+                                          (int)top_k, idx, s),
+                       what);
+  }
   if (st) return st;
   const bool sched = lcv::schedule_supported((int)nb, (int)nb);
   if (sched) {
-    st = launch_status(lcv::launch_schedule(idx, (int)(B * H), (int)nb, (int)nb, (int)top_k, order, s),
-                       "lcv_bsa_forward(schedule)");
+    snprintf(what, sizeof(what), "%s(schedule)", name);
+    st = launch_status(lcv::launch_schedule(idx, (int)(B * H), (int)nb, (int)nb, (int)top_k, order,
+                                            s),
+                       what);
     if (st) return st;
   }
   const lcv::AttnParams p = make_attn_params(q, k, v, out, qs, ks, vs, os, idx,
                                              sched ? order : nullptr, B, H, S, D, dtype, nb, nb,
                                              top_k, sm_scale, g, g);
-  return launch_status(lcv::launch_attn(p, dtype, (int)D, s), "lcv_bsa_forward(attn)");
+  snprintf(what, sizeof(what), "%s(attn)", name);
+  return launch_status(lcv::launch_attn(p, dtype, (int)D, s), what);
+}
+
+// ---------------------------------------------------------------------------
+// Device scratch of lcv_bsa_forward_noalloc: the pooled means of q and k and
+// the launch order, in a file-scope array that every GPU the library runs on
+// holds (its own copy) until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is a stand-in, not a device
+// address): the device address comes from hipGetSymbolAddress, once per
+// device, with that device current, and is kept per device.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = size_t{64} << 20;  // LCV_BSA_NOALLOC_SCRATCH_BYTES
+static_assert(kNoAllocScratchBytes == LCV_BSA_NOALLOC_SCRATCH_BYTES, "header and library agree");
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(LCV_BSA_ERR_LAUNCH, "lcv_bsa_forward_noalloc: hipGetDevice: %s",
+                hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "lcv_bsa_forward_noalloc: device %d beyond %d", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(LCV_BSA_ERR_LAUNCH, "lcv_bsa_forward_noalloc: hipGetSymbolAddress(scratch) on "
+                  "device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LCV_BSA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                    int64_t S, int64_t D, lcv_bsa_strides qs, lcv_bsa_strides ks,
+                    lcv_bsa_strides vs, int64_t top_k, float sm_scale, lcv_bsa_geom g,
+                    void* workspace, size_t workspace_bytes, int32_t* idx, void* out,
+                    lcv_bsa_strides os, void* stream) {
+  int64_t nb = 0, bs = 0;
+  int st = check_forward_args(q, k, v, dtype, B, H, S, D, qs, ks, vs, top_k, sm_scale, g, idx, out,
+                              os, &nb, &bs);
+  if (st) return st;
+  if (!workspace) return fail(LCV_BSA_ERR_INVALID_ARG, "null workspace pointer");
+  const size_t need = lcv_bsa_forward_workspace_bytes(B, H, nb, D);
+  if (workspace_bytes < need || ((uintptr_t)workspace & 255u))
+    return fail(LCV_BSA_ERR_INVALID_ARG,
+                "workspace must be 256-byte aligned and hold %zu bytes (got %zu)", need,
+                workspace_bytes);
+  const size_t pb = pooled_bytes(B, H, nb, D);
+  char* ws = reinterpret_cast<char*>(workspace);
+  return run_forward(q, k, v, dtype, B, H, S, D, qs, ks, vs, top_k, sm_scale, g, nb, bs,
+                     reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws + pb),
+                     reinterpret_cast<float*>(ws + 2 * pb),
+                     reinterpret_cast<int32_t*>(ws + 2 * pb + score_bytes(B, H, nb)), idx, out, os,
+                     (hipStream_t)stream, "lcv_bsa_forward");
+}
+
+int lcv_bsa_forward_noalloc(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                            int64_t H, int64_t S, int64_t D, lcv_bsa_strides qs,
+                            lcv_bsa_strides ks, lcv_bsa_strides vs, int64_t top_k,
+                            float sm_scale, lcv_bsa_geom g, int32_t* idx, void* out,
+                            lcv_bsa_strides os, void* stream) {
+  int64_t nb = 0, bs = 0;
+  int st = check_forward_args(q, k, v, dtype, B, H, S, D, qs, ks, vs, top_k, sm_scale, g, idx, out,
+                              os, &nb, &bs);
+  if (st) return st;
+  // Every size is checked before the device is touched.
+  const size_t pb = pooled_bytes(B, H, nb, D);
+  const size_t need = 2 * pb + align256((size_t)B * H * nb * sizeof(int32_t));
+  if (need > kNoAllocScratchBytes)
+    return fail(LCV_BSA_ERR_UNSUPPORTED,
+                "lcv_bsa_forward_noalloc: the pooled means and launch order of B=%lld H=%lld "
+                "num_blocks=%lld D=%lld need %zu bytes, beyond its fixed device scratch of %zu "
+                "bytes; call lcv_bsa_forward with a workspace instead",
+                (long long)B, (long long)H, (long long)nb, (long long)D, need,
+                kNoAllocScratchBytes);
+  void* base = nullptr;
+  if ((st = scratch_on_current_device(&base))) return st;
+  char* ws = reinterpret_cast<char*>(base);
+  return run_forward(q, k, v, dtype, B, H, S, D, qs, ks, vs, top_k, sm_scale, g, nb, bs,
+                     reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws + pb), nullptr,
+                     reinterpret_cast<int32_t*>(ws + 2 * pb), idx, out, os, (hipStream_t)stream,
+                     "lcv_bsa_forward_noalloc");
 }
 
 int lcv_bsa_block_rows(const void* x, const void* a, int dtype, int64_t B, int64_t N, int64_t C,

@@ -76,6 +76,9 @@ _SIGNATURES = {
     "lcv_bsa_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
                                 c_int64, Strides, Strides, Strides, c_int64, c_float, Geom,
                                 c_void_p, c_size_t, c_void_p, c_void_p, Strides, c_void_p]),
+    "lcv_bsa_forward_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
+                                        c_int64, Strides, Strides, Strides, c_int64, c_float, Geom,
+                                        c_void_p, c_void_p, Strides, c_void_p]),
     "lcv_bsa_token_blocks": (c_int, [Geom, c_void_p, c_void_p]),
     "lcv_bsa_token_pair_mask": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p,
                                         c_int64, c_int64, c_void_p, c_void_p]),
