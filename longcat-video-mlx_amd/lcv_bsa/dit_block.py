@@ -71,7 +71,8 @@ def modulate_fp32(norm: LayerNorm_FP32, x: torch.Tensor, shift: torch.Tensor, sc
     """``norm(x.float()) * (scale + 1) + shift`` in fp32, cast to x's dtype
     (blocks.py:106-119); shift / scale must be fp32."""
     assert shift.dtype == torch.float32 and scale.dtype == torch.float32, (
-        "Modulation params must be fp32; AdaLN math diverges in bf16.")
+        f"modulate_fp32 takes fp32 shift and scale (got {shift.dtype} and {scale.dtype}): "
+        "the AdaLN modulation is computed in fp32")
     return (norm(x.float()) * (scale + 1) + shift).to(x.dtype)
 
 
