@@ -1,8 +1,12 @@
-// Block routing: fp32 block scores qbar . kbar^T and per-row top-k.
+// Block routing: block scores qbar . kbar^T of fp32 pooled means and per-row
+// top-k.
 //
-// The score GEMM runs on fp32 MFMA for head dims 64 and 128 (nk <= 2048) and
-// on fp32 FMAs otherwise; either way each score is an fp32 dot product, and
-// selection is exact given score margins well above fp32 rounding.
+// For head dims 64 and 128 the score GEMM runs on bf16 MFMA with each fp32
+// operand split exactly into three bf16 pieces (six piece products, fp32
+// accumulation; see below): every product is formed to within 2^-21 of its
+// value and the sum is accumulated in fp32, an error of the order of an fp32
+// GEMM's.  Other head dims use fp32 FMAs.  Selection is exact given score
+// margins well above that rounding.
 //
 // Follows block_routing_scores + topk_block_indices
 // (longcat_video/models/block_sparse_attention.py:107-134).  The reference
@@ -64,25 +68,50 @@ __device__ uint32_t kth_key(const uint32_t (&key)[R], int k, uint32_t floor) {
   return thr;
 }
 
-template <int R>
-__device__ uint32_t kth_key_compacted(const uint32_t* buf, int total, int k, uint32_t floor) {
+
+// Emits, in ascending column order, the k selected entries among R keys per
+// lane at list positions lane + 64 r (r < R; positions >= n are not keys):
+// those above thr, then the lowest-positioned ones equal to it.  Positions
+// must follow ascending column order; col(r) gives the column of register r.
+template <int R, typename ColFn>
+__device__ __forceinline__ void emit_selected(const uint32_t (&key)[R], int n, uint32_t thr, int k,
+                                              int32_t* out, ColFn col) {
   const int lane = lane_id();
-  uint32_t key[R];
+  int gt = 0;
 #pragma unroll
-  for (int r = 0; r < R; ++r) key[r] = lane + 64 * r < total ? buf[lane + 64 * r] : 0u;
-  return kth_key<R>(key, k, floor);
+  for (int r = 0; r < R; ++r) gt += __popcll(ballot64(lane + 64 * r < n && key[r] > thr));
+  const int need_eq = k - gt;
+  int run_sel = 0, run_eq = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const bool valid = lane + 64 * r < n;
+    const bool is_gt = valid && key[r] > thr;
+    const bool is_eq = valid && key[r] == thr;
+    const uint64_t eqm = ballot64(is_eq);
+    const int eq_rank = run_eq + (int)mbcnt64(eqm);
+    const bool sel = is_gt || (is_eq && eq_rank < need_eq);
+    const uint64_t selm = ballot64(sel);
+    if (sel) out[run_sel + (int)mbcnt64(selm)] = col(r);
+    run_sel += __popcll(selm);
+    run_eq += __popcll(eqm);
+  }
 }
+
+// Compacted keys a wave keeps for a row of NPER keys per lane.
+template <int NPER>
+constexpr int compact_cap() { return NPER * 64 < kCompactCap ? NPER * 64 : kCompactCap; }
 
 // Exact top-k of one score row held as sc[e] = score[e*64 + lane], e < NPER.
 // Writes the k selected column indices, ascending, to out[0..k).  buf:
-// kCompactCap words of this wave's LDS.
+// 2 compact_cap<NPER>() words of this wave's LDS (keys, then their columns).
 //
 // For k <= 64 (and nk >= 64) a lower bound on the k-th largest key comes
 // first: every lane's largest key is >= L = their minimum, so at least
 // 64 >= k keys are >= L and the k-th largest key is among the keys >= L.
-// Those (typically a quarter of the row) are compacted into 4 or 8
-// registers per lane and searched there; counts at candidates >= L equal
-// the full row's, below L both are >= k, so the threshold is the full row's.
+// Those (typically a quarter of the row) are compacted, in column order,
+// with their columns, into 4 or 8 registers per lane; the search and the
+// emission then run over them only (counts at candidates >= L equal the full
+// row's, below L both are >= k, so the threshold is the full row's).
 template <int NPER>
 __device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out, uint32_t* buf) {
   const int lane = lane_id();
@@ -92,8 +121,7 @@ __device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out, 
     const int col = e * 64 + lane;
     key[e] = col < nk ? order_key(sc[e]) : 0u;
   }
-  uint32_t thr = 0u;
-  bool found = false;
+  constexpr int CAP = compact_cap<NPER>();
   if (k <= 64 && nk >= 64) {  // wave-uniform
     uint32_t lane_max = 0u;
 #pragma unroll
@@ -105,38 +133,31 @@ __device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out, 
       const bool in = e * 64 + lane < nk && key[e] >= L;
       const uint64_t msk = ballot64(in);
       const int pos = total + (int)mbcnt64(msk);
-      if (in && pos < kCompactCap) buf[pos] = key[e];
+      if (in && pos < CAP) {
+        buf[pos] = key[e];
+        buf[CAP + pos] = (uint32_t)(e * 64 + lane);
+      }
       total += __popcll(msk);
     }
     if (total <= 256) {
-      thr = kth_key_compacted<4>(buf, total, k, L);
-      found = true;
-    } else if (total <= kCompactCap) {
-      thr = kth_key_compacted<8>(buf, total, k, L);
-      found = true;
+      uint32_t ck[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ck[r] = lane + 64 * r < total ? buf[lane + 64 * r] : 0u;
+      const uint32_t thr = kth_key<4>(ck, k, L);
+      emit_selected<4>(ck, total, thr, k, out, [&](int r) { return (int32_t)buf[CAP + lane + 64 * r]; });
+      return;
+    }
+    if (total <= CAP) {
+      uint32_t ck[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) ck[r] = lane + 64 * r < total ? buf[lane + 64 * r] : 0u;
+      const uint32_t thr = kth_key<8>(ck, k, L);
+      emit_selected<8>(ck, total, thr, k, out, [&](int r) { return (int32_t)buf[CAP + lane + 64 * r]; });
+      return;
     }
   }
-  if (!found) thr = kth_key<NPER>(key, k, 0u);
-
-  int gt = 0;
-#pragma unroll
-  for (int e = 0; e < NPER; ++e) gt += __popcll(ballot64(key[e] > thr));
-  const int need_eq = k - gt;
-  int run_sel = 0, run_eq = 0;
-#pragma unroll
-  for (int e = 0; e < NPER; ++e) {
-    const int col = e * 64 + lane;
-    const bool valid = col < nk;
-    const bool is_gt = valid && key[e] > thr;
-    const bool is_eq = valid && key[e] == thr;
-    const uint64_t eqm = ballot64(is_eq);
-    const int eq_rank = run_eq + (int)mbcnt64(eqm);
-    const bool sel = is_gt || (is_eq && eq_rank < need_eq);
-    const uint64_t selm = ballot64(sel);
-    if (sel) out[run_sel + (int)mbcnt64(selm)] = col;
-    run_sel += __popcll(selm);
-    run_eq += __popcll(eqm);
-  }
+  const uint32_t thr = kth_key<NPER>(key, k, 0u);
+  emit_selected<NPER>(key, nk, thr, k, out, [&](int r) { return (int32_t)(r * 64 + lane); });
 }
 
 struct RouteArgs {
@@ -160,7 +181,7 @@ template <int NPER, int RW, int MODE>
 __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   __shared__ __attribute__((aligned(16))) float kch[kKeyChunk * (kMaxD + 4)];
   __shared__ __attribute__((aligned(16))) float qt[4 * RW * kMaxD];
-  __shared__ uint32_t tk_buf[4][kCompactCap];
+  __shared__ uint32_t tk_buf[4][2 * kCompactCap];
   const int tid = threadIdx.x;
   const int wave = tid / 64;
   const int lane = tid % 64;
@@ -250,71 +271,239 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   }
 }
 
-// Score rows on fp32 MFMA (v_mfma_f32_16x16x4_f32).  One workgroup = 16
-// q-block rows of one (b, h); wave w computes the 16-column score tiles
-// w, w + 4, ... .  Operands come straight from global memory into registers:
-// k-step s = 4 s4 + u of lane (c, kg) (c = lane % 16, kg = lane / 16) pairs
-// dim 16 s4 + 4 kg + u of q-block row c (A) and of key row 16t + c (B), so
-// the four kg lanes of a row load 64 contiguous bytes per instruction (16
-// cache lines per wave load, not 64).  The accumulator holds
-// S[4kg + i][16t + c].  The 16 x nk score rows are gathered in LDS and each
-// wave runs wave_topk on four of them: routing without a score buffer.
+// ---------------------------------------------------------------------------
+// Score GEMM for head dims 64 and 128 on bf16 MFMA (v_mfma_f32_32x32x16_bf16)
+// with fp32 operands split exactly into three bf16 pieces.
+//
+// A finite fp32 x has 24 significand bits; p0 = x with the low 16 bits of its
+// encoding cleared (the top 8 significand bits), p1 the same truncation of
+// x - p0, and p2 = x - p0 - p1 (at most 8 significand bits, exactly a bf16).
+// Every subtraction is exact, so x = p0 + p1 + p2.  A product x y is formed
+// from the six piece products p_i q_j with i + j <= 2; each is exact in fp32
+// (8 x 8 bits), and the three dropped ones (i + j >= 3) are below
+// 2^-21 |x y| together.  The MFMAs accumulate the six products of every
+// 16-dim k-step into one fp32 accumulator, k-steps ascending, in the order
+// p0q0, p0q1, p1q0, p0q2, p1q1, p2q0.  Both kernels below issue that MFMA
+// sequence per score with the same lane layout (lane (c, g) of a 32 x 16
+// operand holds dims 16s + 8g .. + 8 of row c), so they produce identical
+// scores.  An inf or NaN goes whole into p0; its product with the other
+// operand's p0 carries it as an fp32 product would, and the cross products
+// take p0 without it (tile_step_nf), so non-finite scores come out as the
+// fp32 GEMM's do.
+// ---------------------------------------------------------------------------
+
+// Pieces of 8 consecutive fp32 values, as three bf16x8 operands.  Finite
+// values only (the callers route blocks holding inf / NaN to split8_any).
+__device__ __forceinline__ void split8(const f32x4& lo, const f32x4& hi, bf16x8 (&pc)[3]) {
+  uint32_t w[3][4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    uint32_t u[2], u1[2], u2[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float x = h < 2 ? lo[2 * h + e] : hi[2 * h - 4 + e];
+      u[e] = __builtin_bit_cast(uint32_t, x);
+      const float r1 = x - __builtin_bit_cast(float, u[e] & 0xffff0000u);
+      u1[e] = __builtin_bit_cast(uint32_t, r1);
+      const float r2 = r1 - __builtin_bit_cast(float, u1[e] & 0xffff0000u);
+      u2[e] = __builtin_bit_cast(uint32_t, r2);
+    }
+    // High halves of the pair: element 2h in the low 16 bits.
+    w[0][h] = __builtin_amdgcn_perm(u[1], u[0], 0x07060302u);
+    w[1][h] = __builtin_amdgcn_perm(u1[1], u1[0], 0x07060302u);
+    w[2][h] = __builtin_amdgcn_perm(u2[1], u2[0], 0x07060302u);
+  }
+#pragma unroll
+  for (int q = 0; q < 3; ++q)
+    pc[q] = __builtin_bit_cast(bf16x8, (u32x4){w[q][0], w[q][1], w[q][2], w[q][3]});
+}
+
+// Any fp32 values: inf and NaN go whole into piece 0 (a NaN stays a NaN in
+// its bf16 high half) with pieces 1 and 2 zero; finite values as split8.
+__device__ __forceinline__ void split8_any(const f32x4& lo, const f32x4& hi, bf16x8 (&pc)[3]) {
+  f32x4 a = lo, b = hi;
+  uint32_t fix[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float x = e < 4 ? a[e] : b[e - 4];
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const bool fin = (u & 0x7f800000u) != 0x7f800000u;
+    // Piece 0 of a non-finite value: its own bits, quiet bit set for a NaN.
+    fix[e] = fin ? 0u : (u | ((u & 0x007fffffu) ? 0x00400000u : 0u));
+    if (e < 4) a[e] = fin ? x : 0.0f; else b[e - 4] = fin ? x : 0.0f;
+  }
+  split8(a, b, pc);
+  uint32_t w0[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const uint32_t f = __builtin_amdgcn_perm(fix[2 * h + 1], fix[2 * h], 0x07060302u);
+    w0[h] = f;
+  }
+  u32x4 p0 = __builtin_bit_cast(u32x4, pc[0]);
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    // Replace the 16-bit halves whose value was non-finite.
+    const uint32_t mlo = fix[2 * h] ? 0x0000ffffu : 0u;
+    const uint32_t mhi = fix[2 * h + 1] ? 0xffff0000u : 0u;
+    p0[h] = (p0[h] & ~(mlo | mhi)) | (w0[h] & (mlo | mhi));
+  }
+  pc[0] = __builtin_bit_cast(bf16x8, p0);
+}
+
+// Bits of element i of a float vector.  The element goes through a scalar
+// first: this compiler bit-casts a vector element subscript passed straight
+// to __builtin_bit_cast as element 0.
+__device__ __forceinline__ uint32_t elem_bits(const f32x4& v, int i) {
+  const float f = v[i];
+  return __builtin_bit_cast(uint32_t, f);
+}
+
+// True when none of the 8 values is inf / NaN.
+__device__ __forceinline__ bool all_finite8(const f32x4& lo, const f32x4& hi) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    m |= ((elem_bits(lo, e) & 0x7f800000u) == 0x7f800000u) ? 1u : 0u;
+    m |= ((elem_bits(hi, e) & 0x7f800000u) == 0x7f800000u) ? 1u : 0u;
+  }
+  return m == 0;
+}
+
+// Pieces of 8 fp32 values, finite or not (wave-uniform choice of path).
+__device__ __forceinline__ void split8_wave(const f32x4& lo, const f32x4& hi, bf16x8 (&pc)[3]) {
+  if (__ballot(!all_finite8(lo, hi)))
+    split8_any(lo, hi, pc);
+  else
+    split8(lo, hi, pc);
+}
+
+// One k-step (16 dims) of a 32 x 32 score tile on v_mfma_f32_32x32x16_bf16:
+// the six piece products in a fixed order (p0 q0, p0 q1, p1 q0, p0 q2, p1 q1,
+// p2 q0) into one fp32 accumulator.
+__device__ __forceinline__ void tile_step(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x16& acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
+}
+
+// Piece 0 with its inf / NaN halves (bf16 exponent all ones) set to zero.
+__device__ __forceinline__ bf16x8 finite_part(const bf16x8& v) {
+  u32x4 w = __builtin_bit_cast(u32x4, v);
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const uint32_t m = w[h] & 0x7f807f80u;
+    if ((m & 0xffffu) == 0x7f80u) w[h] &= 0xffff0000u;
+    if ((m >> 16) == 0x7f80u) w[h] &= 0x0000ffffu;
+  }
+  return __builtin_bit_cast(bf16x8, w);
+}
+
+// tile_step for operands that may hold inf / NaN (in piece 0; pieces 1 and 2
+// of such values are zero).  The product of the two pieces 0 carries them as
+// an fp32 product would; the cross products take piece 0 without them, so
+// no inf meets a zero piece of the other operand.  For finite operands the
+// values, and so the result, are those of tile_step.
+__device__ __forceinline__ void tile_step_nf(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x16& acc) {
+  // Opaque copies: the finite parts are formed here, on this rare path, and
+  // not hoisted next to the operands they come from (they would hold
+  // registers for the whole kernel).
+  bf16x8 a0 = a[0], b0 = b[0];
+  asm volatile("" : "+v"(a0), "+v"(b0));
+  a0 = finite_part(a0);
+  b0 = finite_part(b0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b0, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b0, acc, 0, 0, 0);
+}
+
+// The A pieces of 32 rows (row0 + lane % 32) for all k-steps: lane (r, g)
+// holds dims 16s + 8g .. + 8 of its row.  Rows at or past `nrows` (and
+// lanes whose row is not below `live`) are zero.
+template <int KST>
+__device__ __forceinline__ bool load_row_pieces(const float* base, int row0, int nrows, int D,
+                                                int live, bf16x8 (&pa)[KST][3]) {
+  const int lane = lane_id();
+  const int r = lane % 32;
+  const int row = row0 + r;
+  const int g = lane / 32;
+  bool fin = true;
+#pragma unroll
+  for (int s = 0; s < KST; ++s) {
+    f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
+    if (r < live && row < nrows) {
+      const float* src = base + (int64_t)row * D + 16 * s + 8 * g;
+      lo = *reinterpret_cast<const f32x4*>(src);
+      hi = *reinterpret_cast<const f32x4*>(src + 4);
+    }
+    fin = fin & all_finite8(lo, hi);
+    split8_wave(lo, hi, pa[s]);
+  }
+  return __ballot(!fin) != 0;
+}
+
+// Fused routing for head dims 64 and 128: one workgroup = 16 q-block rows of
+// one (b, h) (the top half of a 32-row MFMA block; the bottom half is zero
+// and discarded); wave w computes the 32-key score tiles w, w + 4, ..., its
+// key operands read from global memory and split in registers.  The 16 x nk
+// score rows are gathered in LDS and each wave runs wave_topk on four of
+// them: routing without a score buffer.
 template <int NPER, int D>
 __global__ __launch_bounds__(256) void select_mfma_kernel(RouteArgs a) {
   constexpr int QR = 16;
-  constexpr int DQ = D / 4;                 // dims per lane group
+  constexpr int KST = D / 16;               // k-steps of 16 dims
   constexpr int LDSW = NPER * 64 + 4;       // score row stride (floats)
-  __shared__ __attribute__((aligned(16))) float srow[QR * LDSW];
-  __shared__ uint32_t tk_buf[4][kCompactCap];
+  // Row stride: the scores, or the top-k buffer the row turns into (2 CAP words).
+  constexpr int RSW = LDSW > 2 * compact_cap<NPER>() ? LDSW : 2 * compact_cap<NPER>();
+  __shared__ __attribute__((aligned(16))) float srow[QR * RSW];
   const int tid = threadIdx.x;
   const int wave = tid / 64;
   const int lane = tid % 64;
-  const int c = lane % 16;
-  const int kg = lane / 16;
+  const int c = lane % 32;
+  const int g = lane / 32;
   const int bh = blockIdx.x / a.tiles_per_bh;
   const int row0 = (blockIdx.x - bh * a.tiles_per_bh) * QR;
   const float* qb = a.qbar + (int64_t)bh * a.nq * D;
   const float* kb = a.kbar + (int64_t)bh * a.nk * D;
 
-  float qa[DQ];
-  {
-    const int row = row0 + c;
+  bf16x8 pa[KST][3];
+  const bool a_bad = load_row_pieces<KST>(qb, row0, a.nq, D, QR, pa);
+  const int ntiles = (a.nk + 31) / 32;
+  for (int t = wave; t < ntiles; t += 4) {
+    const int key = 32 * t + c;
+    f32x16 acc;
 #pragma unroll
-    for (int s4 = 0; s4 < DQ / 4; ++s4) {
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      if (row < a.nq) v = *reinterpret_cast<const f32x4*>(qb + (int64_t)row * D + 16 * s4 + 4 * kg);
+    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+    // tile_step_nf equals tile_step on finite operands, so the (wave-uniform)
+    // choice can be made per k-step.
 #pragma unroll
-      for (int u = 0; u < 4; ++u) qa[4 * s4 + u] = v[u];
+    for (int s = 0; s < KST; ++s) {
+      f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
+      if (key < a.nk) {
+        const float* src = kb + (int64_t)key * D + 16 * s + 8 * g;
+        lo = *reinterpret_cast<const f32x4*>(src);
+        hi = *reinterpret_cast<const f32x4*>(src + 4);
+      }
+      const bool b_bad = __ballot(!all_finite8(lo, hi)) != 0;
+      bf16x8 pb[3];
+      if (b_bad)
+        split8_any(lo, hi, pb);
+      else
+        split8(lo, hi, pb);
+      if (a_bad || b_bad)
+        tile_step_nf(pa[s], pb, acc);
+      else
+        tile_step(pa[s], pb, acc);
     }
-  }
-  const int ntiles = (a.nk + 15) / 16;
-  auto load_b = [&](int t, float (&kv)[DQ]) {
-    const int key = 16 * t + c;
+    // Rows 8 (i / 4) + 4 g + i % 4 of the tile; i < 8 are the 16 live rows.
 #pragma unroll
-    for (int s4 = 0; s4 < DQ / 4; ++s4) {
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      if (key < a.nk) v = *reinterpret_cast<const f32x4*>(kb + (int64_t)key * D + 16 * s4 + 4 * kg);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) kv[4 * s4 + u] = v[u];
-    }
-  };
-  float kv0[DQ], kv1[DQ];
-  int t = wave;
-  if (t < ntiles) load_b(t, kv0);
-  auto tile = [&](int tt, const float (&kv)[DQ]) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < DQ; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], kv[s], acc, 0, 0, 0);
-    const int col = 16 * tt + c;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) srow[(4 * kg + i) * LDSW + col] = acc[i];
-  };
-  for (; t < ntiles; t += 8) {
-    if (t + 4 < ntiles) load_b(t + 4, kv1);
-    tile(t, kv0);
-    if (t + 4 >= ntiles) break;
-    if (t + 8 < ntiles) load_b(t + 8, kv0);
-    tile(t + 4, kv1);
+    for (int i = 0; i < 8; ++i)
+      srow[(8 * (i / 4) + 4 * g + i % 4) * RSW + 32 * t + c] = acc[i];
   }
   __syncthreads();
 #pragma unroll 1
@@ -323,127 +512,137 @@ __global__ __launch_bounds__(256) void select_mfma_kernel(RouteArgs a) {
     if (row >= a.nq) break;  // wave-uniform; rows only grow
     float sc[NPER];
 #pragma unroll
-    for (int e = 0; e < NPER; ++e) sc[e] = srow[r * LDSW + e * 64 + lane];
+    for (int e = 0; e < NPER; ++e) sc[e] = srow[r * RSW + e * 64 + lane];
+    // The row's LDS, now in registers, becomes this wave's top-k buffer (LDS
+    // operations of one wave complete in order; the fence keeps the
+    // compiler from moving the buffer's writes above the row's reads).
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     wave_topk<NPER>(sc, a.nk, a.top_k, a.idx + ((int64_t)bh * a.nq + row) * a.top_k,
-                    tk_buf[wave]);
+                    reinterpret_cast<uint32_t*>(&srow[r * RSW]));
   }
 }
 
-// Score matrix S = qbar kbar^T on fp32 MFMA (v_mfma_f32_16x16x4_f32), written
-// to memory.  One workgroup = 4 waves x 16 q-block rows (64 rows) of one
-// (b, h) over a range of 64-key chunks (col_splits ranges per row tile, so
-// that small heads still fill the GPU).  A chunk's kbar rows are staged in
-// LDS (row stride D + 4 floats: the 16-byte operand reads are conflict free)
-// from coalesced 16-byte loads, which for the next chunk are in flight while
-// the current chunk's MFMAs run.  Each wave keeps its rows' qbar in
-// registers and runs the chunk's four 16-key tiles as four interleaved MFMA
-// chains.  k-step s = 4 s4 + u of lane (c, kg) pairs dim 16 s4 + 4 kg + u of
-// q-block row c and of key row 16t + c; the accumulator holds
-// S[4kg + i][16t + c].
+// Score matrix S = qbar kbar^T, written to memory.  One workgroup = 4 waves x
+// 32 q-block rows (128 rows) of one (b, h) over a range of 64-key chunks
+// (col_splits ranges per row tile, so that small heads still fill the GPU).
+// Each wave keeps the pieces of its 32 rows in registers.  A chunk's kbar rows
+// are read with 16-byte buffer loads (the next chunk's in flight during the
+// current chunk's MFMAs; keys past nk read as zero), split, and stored as
+// bf16 pieces in LDS (row stride 2D + 16 bytes: the 16-byte operand reads of
+// 16 consecutive rows are conflict free); each wave then runs the chunk's two
+// 32-key tiles as two interleaved accumulator chains.  Scores go out as
+// buffer stores whose offset is pushed out of range for entries past nq or
+// nk, so every chunk issues the same memory instructions.
 template <int D>
 __global__ __launch_bounds__(256) void scores_kernel(RouteArgs a) {
   constexpr int KC = 64;              // keys per chunk
-  constexpr int KS = D + 4;           // LDS row stride (floats)
-  constexpr int DQ = D / 4;           // k-steps per tile
-  constexpr int D4 = D / 4;           // 16-byte pieces per row
-  constexpr int kLoads = KC * D4 / 256;
-  static_assert(kLoads * 256 == KC * D4, "chunk loads split evenly over the workgroup");
-  __shared__ __attribute__((aligned(16))) float kch[KC * KS];
+  constexpr int KST = D / 16;         // k-steps of 16 dims
+  constexpr int RS = 2 * D + 16;      // LDS row stride of a piece (bytes)
+  constexpr int D8 = D / 8;           // 8-value groups per row
+  constexpr int kGroups = KC * D8 / 256;
+  static_assert(kGroups * 256 == KC * D8, "chunk groups split evenly over the workgroup");
+  __shared__ __attribute__((aligned(16))) uint8_t kp[3][KC * RS];
   const int tid = threadIdx.x;
   const int wave = tid / 64;
   const int lane = tid % 64;
-  const int c = lane % 16;
-  const int kg = lane / 16;
+  const int c = lane % 32;
+  const int g = lane / 32;
   const int per_bh = a.tiles_per_bh * a.col_splits;
   const int bh = blockIdx.x / per_bh;
   const int rem = blockIdx.x - bh * per_bh;
   const int rt = rem / a.col_splits;
   const int cs = rem - rt * a.col_splits;
-  const int row0 = rt * 64 + wave * 16;
+  const int row0 = rt * 128 + wave * 32;
   const int nchunks = (a.nk + KC - 1) / KC;
   const int ch0 = (int)((int64_t)cs * nchunks / a.col_splits);
   const int ch1 = (int)((int64_t)(cs + 1) * nchunks / a.col_splits);
   const float* qb = a.qbar + (int64_t)bh * a.nq * D;
-  const float* kb = a.kbar + (int64_t)bh * a.nk * D;
-  float* so = a.score_out + (int64_t)bh * a.nq * a.nk;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.kbar + (int64_t)bh * a.nk * D), (short)0, a.nk * D * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.score_out + (int64_t)bh * a.nq * a.nk), (short)0, a.nq * a.nk * 4, 0x00020000);
 
-  float qa[DQ];
-  {
-    const int row = row0 + c;
-#pragma unroll
-    for (int s4 = 0; s4 < DQ / 4; ++s4) {
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      if (row < a.nq) v = *reinterpret_cast<const f32x4*>(qb + (int64_t)row * D + 16 * s4 + 4 * kg);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) qa[4 * s4 + u] = v[u];
-    }
-  }
-  f32x4 st[kLoads];
+  bf16x8 pa[KST][3];
+  const bool a_bad = load_row_pieces<KST>(qb, row0, a.nq, D, 32, pa);
+
+  // Staging: group i = tid + 256 u of a chunk is key i / D8, dims 8 (i % D8) .. + 8.
+  f32x4 st[kGroups][2];
   auto load_chunk = [&](int ch) {
 #pragma unroll
-    for (int u = 0; u < kLoads; ++u) {
+    for (int u = 0; u < kGroups; ++u) {
       const int i = tid + 256 * u;
-      const int key = ch * KC + i / D4;
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      if (key < a.nk) v = *reinterpret_cast<const f32x4*>(kb + (int64_t)key * D + 4 * (i % D4));
-      st[u] = v;
+      const uint32_t off = (uint32_t)((ch * KC + i / D8) * D + 8 * (i % D8)) * 4u;
+      st[u][0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
+      st[u][1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, off + 16, 0, 0));
     }
   };
+  constexpr uint32_t kDrop = 0x80000000u;  // out-of-range offset: the store is dropped
   if (ch0 < ch1) load_chunk(ch0);
   for (int ch = ch0; ch < ch1; ++ch) {
     __syncthreads();  // the previous chunk is consumed
+    bool fin = true;
+    {
 #pragma unroll
-    for (int u = 0; u < kLoads; ++u) {
-      const int i = tid + 256 * u;
-      *reinterpret_cast<f32x4*>(kch + (i / D4) * KS + 4 * (i % D4)) = st[u];
-    }
-    __syncthreads();
-    if (ch + 1 < ch1) load_chunk(ch + 1);
-    f32x4 acc[4];
+      for (int u = 0; u < kGroups; ++u) fin = fin & all_finite8(st[u][0], st[u][1]);
+      const bool any_bad = __ballot(!fin) != 0;  // wave-uniform
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    // The key operands of step s4 + 1 are read while the MFMAs of step s4
-    // run (scheduling groups keep the compiler from sinking the reads).
-    f32x4 kv[2][4];
-    auto read_kv = [&](int s4, f32x4* dst) {
+      for (int u = 0; u < kGroups; ++u) {
+        const int i = tid + 256 * u;
+        bf16x8 pc[3];
+        if (any_bad)
+          split8_any(st[u][0], st[u][1], pc);
+        else
+          split8(st[u][0], st[u][1], pc);
+        const int off = (i / D8) * RS + 16 * (i % D8);
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        dst[t] = *reinterpret_cast<const f32x4*>(kch + (16 * t + c) * KS + 16 * s4 + 4 * kg);
-    };
-    read_kv(0, kv[0]);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
-#pragma unroll
-    for (int s4 = 0; s4 < DQ / 4; ++s4) {
-      if (s4 + 1 < DQ / 4) read_kv(s4 + 1, kv[(s4 + 1) & 1]);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[4 * s4 + u], kv[s4 & 1][t][u], acc[t], 0,
-                                                        0, 0);
-        if (s4 + 1 < DQ / 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA
+        for (int q = 0; q < 3; ++q) *reinterpret_cast<bf16x8*>(&kp[q][off]) = pc[q];
       }
     }
-    // Scores: rows row0 + 4kg + i, columns ch*64 + 16t + c.  Interior tiles
-    // store without per-element checks.
-    float* srow = so + (int64_t)(row0 + 4 * kg) * a.nk + ch * KC + c;
-    if (row0 + 16 <= a.nq && (ch + 1) * KC <= a.nk) {
+    // Barrier (every thread reaches it); true when any thread staged an inf / NaN.
+    const bool chunk_bad = __syncthreads_or(!fin) != 0;
+    const bool bad = a_bad || chunk_bad;
+    if (ch + 1 < ch1) load_chunk(ch + 1);
+    f32x16 acc[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) srow[(int64_t)i * a.nk + 16 * t] = acc[t][i];
+      for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+    bf16x8 pb[2][3];
+    auto read_b = [&](int s, int t, bf16x8 (&dst)[3]) {
+      const int off = (32 * t + c) * RS + 32 * s + 16 * g;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) dst[q] = *reinterpret_cast<const bf16x8*>(&kp[q][off]);
+    };
+    if (!bad) {
+      read_b(0, 0, pb[0]);
+#pragma unroll
+      for (int s = 0; s < KST; ++s) {
+        read_b(s, 1, pb[1]);
+        tile_step(pa[s], pb[0], acc[0]);
+        if (s + 1 < KST) read_b(s + 1, 0, pb[0]);
+        tile_step(pa[s], pb[1], acc[1]);
+      }
     } else {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int col = ch * KC + 16 * t + c;
-        if (col < a.nk) {
+      for (int s = 0; s < KST; ++s) {
+        read_b(s, 0, pb[0]);
+        read_b(s, 1, pb[1]);
+        tile_step_nf(pa[s], pb[0], acc[0]);
+        tile_step_nf(pa[s], pb[1], acc[1]);
+      }
+    }
+    // Scores: rows row0 + 8 (i / 4) + 4 g + i % 4, columns ch * 64 + 32 t + c.
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int row = row0 + 4 * kg + i;
-            if (row < a.nq) so[(int64_t)row * a.nk + col] = acc[t][i];
-          }
-        }
+    for (int t = 0; t < 2; ++t) {
+      const int col = ch * KC + 32 * t + c;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = row0 + 8 * (i / 4) + 4 * g + i % 4;
+        const uint32_t off = (row < a.nq && col < a.nk) ? (uint32_t)(row * a.nk + col) * 4u : kDrop;
+        // Through a scalar: a vector element subscript passed straight to
+        // __builtin_bit_cast is read as element 0 by this compiler.
+        const float v = acc[t][i];
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), srs, off, 0, 0);
       }
     }
   }
@@ -451,10 +650,10 @@ __global__ __launch_bounds__(256) void scores_kernel(RouteArgs a) {
 
 template <int D>
 hipError_t launch_scores_mfma(RouteArgs a, int BH, hipStream_t stream) {
-  a.tiles_per_bh = (a.nq + 63) / 64;
+  a.tiles_per_bh = (a.nq + 127) / 128;
   const int nchunks = (a.nk + 63) / 64;
   const int base = BH * a.tiles_per_bh;
-  int splits = (1024 + base - 1) / base;  // about four workgroups per CU
+  int splits = (512 + base - 1) / base;  // about two workgroups per CU: one round
   a.col_splits = splits < nchunks ? splits : nchunks;
   hipLaunchKernelGGL((scores_kernel<D>), dim3(base * a.col_splits), dim3(256), 0, stream, a);
   return hipGetLastError();

@@ -121,6 +121,53 @@ def test_scores_match_oracle(device, nq, nk, D):
     assert_close_report(got, ref, 2e-5 * math.sqrt(D), 2e-6 * math.sqrt(D), f"scores {nq}x{nk}x{D}")
 
 
+@pytest.mark.parametrize("nq,nk,D", [(900, 900, 128), (450, 450, 64), (65, 2049, 128)])
+def test_scores_error_within_piece_bound(device, nq, nk, D):
+    """The bf16-piece GEMM drops only piece products below 2^-21 |x y|
+    together and accumulates in fp32: against fp64, every score is within
+    2e-6 of sum_d |x_d y_d|.  Dropping one kept product (2^-8 |x y|) or
+    truncating an operand to bf16 would miss by three orders of magnitude."""
+    from lcv_bsa import block_routing_scores
+
+    qb = _rand((1, 2, nq, D), torch.float32, device, seed=11 * nq) * 0.7 + 0.2
+    kb = _rand((1, 2, nk, D), torch.float32, device, seed=13 * nk) * 0.4 - 0.1
+    got = block_routing_scores(qb, kb).double()
+    q64, k64 = qb.double(), kb.double()
+    ref = torch.matmul(q64, k64.transpose(-1, -2))
+    env = torch.matmul(q64.abs(), k64.abs().transpose(-1, -2))
+    ratio = ((got - ref).abs() / env).max().item()
+    print(f"scores {nq}x{nk}x{D}: max |err| / envelope = {ratio:.2e}")
+    assert ratio <= 2e-6
+
+
+def test_scores_nonfinite_like_fp32(device):
+    """inf / NaN in the pooled means: every score is NaN, +inf or -inf exactly
+    where the fp32 GEMM's is (an inf meets no zero piece of the other
+    operand), the finite ones stay within fp32 rounding, and the fused
+    routing still equals scores + top-k."""
+    from lcv_bsa import block_routing_scores, select_block_indices, topk_block_indices
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    for nq, nk, D, k in [(100, 300, 128, 19), (70, 200, 64, 12), (33, 129, 128, 64)]:
+        qb = _rand((1, 2, nq, D), torch.float32, device, seed=nq)
+        kb = _rand((1, 2, nk, D), torch.float32, device, seed=nk)
+        qb[0, 0, 3, 5] = float("inf")
+        qb[0, 0, 7, 9] = float("-inf")
+        qb[0, 0, 11, 2] = float("nan")
+        qb[0, 0, 13, 4], qb[0, 0, 13, 6] = float("inf"), float("-inf")
+        kb[0, 0, 17, 8] = float("inf")
+        kb[0, 0, 20, 1] = float("nan")
+        kb[0, 1, 40, 3] = float("-inf")
+        got = block_routing_scores(qb, kb)
+        ref = torch.matmul(qb, kb.transpose(-1, -2))
+        for cls in (torch.isnan, torch.isposinf, torch.isneginf):
+            assert torch.equal(cls(got), cls(ref)), (nq, nk, D, cls.__name__)
+        fin = torch.isfinite(ref)
+        assert (got[fin] - ref[fin]).abs().max().item() <= 2e-5 * math.sqrt(D)
+        two, _ = topk_block_indices(got, 0.0, top_k=k)
+        assert torch.equal(select_block_indices(qb, kb, k, fused=True), two)
+
+
 def test_scores_known_answer(device):
     """test_bsa_tier_a_smoke.py:68-75."""
     from lcv_bsa import block_routing_scores
