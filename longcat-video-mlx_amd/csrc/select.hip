@@ -108,10 +108,12 @@ constexpr int compact_cap() { return NPER * 64 < kCompactCap ? NPER * 64 : kComp
 // For k <= 64 (and nk >= 64) a lower bound on the k-th largest key comes
 // first: every lane's largest key is >= L = their minimum, so at least
 // 64 >= k keys are >= L and the k-th largest key is among the keys >= L.
-// Those (typically a quarter of the row) are compacted, in column order,
-// with their columns, into 4 or 8 registers per lane; the search and the
-// emission then run over them only (counts at candidates >= L equal the full
-// row's, below L both are >= k, so the threshold is the full row's).
+// For 64 < k <= 128 (and nk >= 128) the lanes' second-largest keys give the
+// bound the same way (at least 128 keys are >= their minimum).  The keys
+// >= L (typically a quarter or a third of the row) are compacted, in column
+// order, with their columns, into 4 or 8 registers per lane; the search and
+// the emission then run over them only (counts at candidates >= L equal the
+// full row's, below L both are >= k, so the threshold is the full row's).
 template <int NPER>
 __device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out, uint32_t* buf) {
   const int lane = lane_id();
@@ -122,11 +124,21 @@ __device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out, 
     key[e] = col < nk ? order_key(sc[e]) : 0u;
   }
   constexpr int CAP = compact_cap<NPER>();
-  if (k <= 64 && nk >= 64) {  // wave-uniform
-    uint32_t lane_max = 0u;
+  if ((k <= 64 && nk >= 64) || (k <= 128 && nk >= 128)) {  // wave-uniform
+    uint32_t m = 0u;  // this lane's largest key (k <= 64) or second-largest key
+    if (k <= 64) {
 #pragma unroll
-    for (int e = 0; e < NPER; ++e) lane_max = key[e] > lane_max ? key[e] : lane_max;
-    const uint32_t L = wave_min_u32(lane_max);
+      for (int e = 0; e < NPER; ++e) m = key[e] > m ? key[e] : m;
+    } else {
+      uint32_t m1 = 0u;
+#pragma unroll
+      for (int e = 0; e < NPER; ++e) {
+        const uint32_t lo = key[e] < m1 ? key[e] : m1;
+        m = lo > m ? lo : m;
+        m1 = key[e] > m1 ? key[e] : m1;
+      }
+    }
+    const uint32_t L = wave_min_u32(m);
     int total = 0;
 #pragma unroll
     for (int e = 0; e < NPER; ++e) {

@@ -199,9 +199,10 @@ def test_topk_exact_with_ties(device, nk):
 
 @pytest.mark.parametrize("nk", [64, 128, 129, 900, 2048])
 def test_topk_lower_bound_paths(device, nk):
-    """k on both sides of 64: the search over the keys above a lower bound
-    (the smallest of the lanes' largest keys) and the full search, on
-    continuous scores and with a third of some rows tied at the top."""
+    """k on both sides of 64 and 128: the search over the keys above a lower
+    bound (the smallest of the lanes' largest keys for k <= 64, of their
+    second-largest keys for k <= 128) and the full search, on continuous
+    scores and with a third of some rows tied at the top."""
     from lcv_bsa import topk_block_indices
 
     rng = np.random.default_rng(100 + nk)
