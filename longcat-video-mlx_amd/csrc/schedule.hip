@@ -12,9 +12,13 @@
 // q-block i's key is (first, median, i), with entries outside [0, nk) (the
 // K/V block count of the head, which exceeds nq when keys outnumber queries)
 // counting as nk.  The key is unique, so the sorted order is a permutation,
-// the same one any correct sort gives.  Two sorts:
-//   * nq <= 1024: one workgroup per head, one key per thread, bitonic; the
-//     stages whose partner lies in the same wave exchange keys with lane
+// the same one any correct sort gives.  Three sorts:
+//   * nq <= 1024 and at most 512 workgroups of 64 keys: a rank sort, i to
+//     position #{j : key_j < key_i}; each workgroup stages the head's keys
+//     in LDS (32-bit when nq, nk <= 1023 fit 10 bits a field), and its four
+//     waves count over a quarter of them each for the same 64 keys;
+//   * other nq <= 1024: one workgroup per head, one key per thread, bitonic;
+//     the stages whose partner lies in the same wave exchange keys with lane
 //     shuffles, the rest through LDS;
 //   * 1024 < nq <= 4096: a rank sort.  i goes to position #{j : key_j <
 //     key_i}; every workgroup stages all keys of its head in LDS and ranks 256
@@ -97,6 +101,53 @@ __global__ __launch_bounds__(kSmallSched) void schedule_small_kernel(const int32
   if (i < nq) order[(int64_t)bh * nq + i] = (int32_t)(key & 0xFFFFFu);
 }
 
+// Rank sort for nq <= 1024 with the key packed into 32 bits when first,
+// median (<= nk) and i fit 10 bits each, else 64.  A workgroup ranks 64 keys
+// of one head: its four waves each count, for the same 64 keys (one per
+// lane), the keys below them in a quarter of the head's staged keys
+// (broadcast LDS reads), and the four partial ranks are summed.  A head's
+// sort is spread over ceil(nq / 64) workgroups.
+template <typename KeyT>
+__device__ __forceinline__ KeyT pack_key(const int32_t* rows, int i, int nk, int top_k);
+template <>
+__device__ __forceinline__ uint32_t pack_key<uint32_t>(const int32_t* rows, int i, int nk, int top_k) {
+  const uint64_t k = order_key(rows, i, nk, top_k);
+  return (uint32_t)(((k >> 40) << 20) | (((k >> 20) & 0xFFFFFu) << 10) | (k & 0xFFFFFu));
+}
+template <>
+__device__ __forceinline__ uint64_t pack_key<uint64_t>(const int32_t* rows, int i, int nk, int top_k) {
+  return order_key(rows, i, nk, top_k);
+}
+
+constexpr int kRankGroup = 64;           // keys ranked per workgroup
+constexpr int kRankSmallMaxWgs = 512;     // rank-sort grid limit (workgroups)
+
+template <typename KeyT>
+__global__ __launch_bounds__(256) void schedule_rank_small_kernel(const int32_t* idx, int nq, int nk,
+                                                                  int top_k, int32_t* order) {
+  __shared__ __attribute__((aligned(16))) KeyT keys[kSmallSched];
+  __shared__ int part[4][kRankGroup];
+  const int bh = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int32_t* rows = idx + (int64_t)bh * nq * top_k;
+  for (int i = tid; i < nq; i += 256) keys[i] = pack_key<KeyT>(rows, i, nk, top_k);
+  __syncthreads();
+  const int wave = tid / 64;
+  const int lane = tid % 64;
+  const int i = blockIdx.y * kRankGroup + lane;
+  const KeyT mine = i < nq ? keys[i] : (KeyT)0;
+  const int span = (nq + 3) / 4;
+  const int j0 = wave * span;
+  const int j1 = j0 + span < nq ? j0 + span : nq;
+  int cnt = 0;
+#pragma unroll 8
+  for (int j = j0; j < j1; ++j) cnt += keys[j] < mine ? 1 : 0;
+  part[wave][lane] = cnt;
+  __syncthreads();
+  if (wave == 0 && i < nq)
+    order[(int64_t)bh * nq + (part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane])] = i;
+}
+
 }  // namespace
 
 bool schedule_supported(int nq, int nk) {
@@ -107,6 +158,20 @@ hipError_t launch_schedule(const int32_t* idx, int BH, int nq, int nk, int top_k
                            hipStream_t stream) {
   if (!schedule_supported(nq, nk) || BH < 1 || top_k < 1) return hipErrorInvalidValue;
   if (nq <= kSmallSched) {
+    const int groups = (nq + kRankGroup - 1) / kRankGroup;
+    // The rank sort stages every key of a head once per workgroup, so it
+    // pays while the grid stays within about two workgroups per CU; larger
+    // grids sort faster with the bitonic kernel.
+    if ((int64_t)BH * groups <= kRankSmallMaxWgs) {
+      const dim3 grid((unsigned)BH, (unsigned)groups);
+      if (nk <= 1023)
+        hipLaunchKernelGGL(schedule_rank_small_kernel<uint32_t>, grid, dim3(256), 0, stream, idx,
+                           nq, nk, top_k, order);
+      else
+        hipLaunchKernelGGL(schedule_rank_small_kernel<uint64_t>, grid, dim3(256), 0, stream, idx,
+                           nq, nk, top_k, order);
+      return hipGetLastError();
+    }
     hipLaunchKernelGGL(schedule_small_kernel, dim3(BH), dim3(kSmallSched), 0, stream, idx, nq, nk,
                        top_k, order);
     return hipGetLastError();

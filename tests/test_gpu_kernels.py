@@ -432,18 +432,22 @@ def _attn_with_order(q, k, v, idx, shape, chunk, order, out=None):
     return out
 
 
-@pytest.mark.parametrize("nb,k", [(1, 1), (7, 3), (64, 4), (900, 57), (1024, 8), (1025, 8), (4096, 5)])
-def test_schedule_permutation_sorted_by_key(device, nb, k):
-    """Both sorts: the in-wave bitonic sort (nb <= 1024) and the rank sort
-    over several workgroups per head (1024 < nb <= 4096); padded entries
-    count as nb."""
+@pytest.mark.parametrize("nb,k,heads", [(1, 1, 2), (7, 3, 2), (64, 4, 2), (900, 57, 2), (1024, 8, 2),
+                                         (900, 57, 40), (1024, 8, 33), (1025, 8, 2), (4096, 5, 2)])
+def test_schedule_permutation_sorted_by_key(device, nb, k, heads):
+    """All three sorts: the rank sort with 64 keys per workgroup (nb <= 1024,
+    at most 512 workgroups; 32-bit keys up to nb = 1023, 64-bit at 1024), the
+    in-wave bitonic sort for larger grids (40 heads x 15 groups, 33 x 16) and
+    the rank sort over several workgroups per head (1024 < nb <= 4096);
+    padded entries count as nb."""
     from lcv_bsa import schedule_block_order
 
-    idx = np.sort(_distinct_indices(1, 2, nb, nb, k, seed=nb), axis=-1)
+    idx = np.sort(_distinct_indices(1, heads, nb, nb, k, seed=nb + heads), axis=-1)
     if nb >= 7:
         idx[0, 0, 3, :] = -1  # padding sorts as nb
+        idx[0, heads - 1, nb - 2, :] = -1
     order = schedule_block_order(torch.from_numpy(idx).to(device)).cpu().numpy()
-    for h in range(2):
+    for h in range(heads):
         assert sorted(order[0, h].tolist()) == list(range(nb))
         first = np.where((idx[0, h, :, 0] >= 0), idx[0, h, :, 0], nb)
         med = np.where((idx[0, h, :, k // 2] >= 0), idx[0, h, :, k // 2], nb)
