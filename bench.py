@@ -49,6 +49,33 @@ def _traffic_from_profiles(workload: str):
     return float(m.group(1)) if m else None
 
 
+def _cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it, with its x86 family / model
+    numbers (virtual machines often report only a generic model name) and
+    the hypervisor flag."""
+    fields = {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if ":" not in line:
+                if fields:
+                    break  # first processor's block only
+                continue
+            key, val = (s.strip() for s in line.split(":", 1))
+            fields.setdefault(key, val)
+    except OSError:
+        pass
+    name = fields.get("model name") or platform.processor() or platform.machine()
+    extra = []
+    if "cpu family" in fields and "model" in fields:
+        fam, model = fields["cpu family"], fields["model"]
+        extra.append(f"x86 family {fam} model {model}")
+        if fields.get("vendor_id") == "AuthenticAMD" and fam == "26":
+            extra.append("Zen 5")
+    if "hypervisor" in fields.get("flags", "").split():
+        extra.append("virtual machine")
+    return f"{name} ({', '.join(extra)})" if extra else name
+
+
 def cpu_baseline(w, budget_s: float):
     """The oracle (fp32 NumPy restatement of Tier A) on a bounded sample of the
     same workload: pooling + routing for the sampled heads, then the gathered
@@ -105,14 +132,7 @@ def cpu_baseline(w, budget_s: float):
     if limiter is not None:
         limiter.restore_original_limits()
     flops = O.executed_flops(1, 1, done_blocks, k, D)
-    cpu = platform.processor() or platform.machine()
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    cpu = _cpu_model()
     return {
         "value": flops / t_total / 1e12,
         "unit": "TFLOP/s",
