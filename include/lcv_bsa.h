@@ -251,14 +251,17 @@ int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype,
  * lcv_bsa_forward without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid allocation).  No counterpart in the
- * reference.  Same arguments and result as lcv_bsa_forward (routing by the
- * fused select kernel, which keeps block scores on chip; the routing is the
- * same as the scores + top-k route).  The pooled means and the launch order
- * live in a fixed device array of LCV_BSA_NOALLOC_SCRATCH_BYTES that every
- * GPU the library runs on holds until the process ends:
+ * reference.  Same arguments and result as lcv_bsa_forward.  The pooled
+ * means and the launch order live in a fixed device array of
+ * LCV_BSA_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds
+ * until the process ends:
  *   2 * round256(B*H*nb*D*4) + round256(B*H*nb*4) <= 64 MiB
  * (B*H*nb <= 65,280 at D = 128: both 720p configurations fit); larger
- * problems get LCV_BSA_ERR_UNSUPPORTED before any device work.  The call
+ * problems get LCV_BSA_ERR_UNSUPPORTED before any device work.  The rest of
+ * the array holds the block scores of as many (b, h) pairs as fit, and the
+ * routing runs as score GEMM + top-k over those slices when at most 8 cover
+ * every head (720p, H=32: 3 slices), else as the fused select kernel that
+ * keeps the scores on chip; every route gives the same routing.  The call
  * allocates and frees nothing.  Calls on one GPU share its array: calls
  * that overlap in time on one GPU (other streams, other threads) race and
  * must be serialised by the caller.  Nothing in the array carries over from

@@ -344,13 +344,15 @@ int check_forward_args(const void* q, const void* k, const void* v, int dtype, i
 
 // pool -> routing -> schedule -> attention on validated arguments.  With a
 // score buffer the routing runs as the score GEMM (each staged key chunk
-// shared by 64 rows) plus the per-row top-k; without one, as the fused
-// select kernel that keeps the scores on chip.  Both give the same routing.
+// shared by 64 rows) plus the per-row top-k, score_bh (b, h) slices at a
+// time (all of them when the buffer holds B*H slices); without one, as the
+// fused select kernel that keeps the scores on chip.  All give the same
+// routing.
 int run_forward(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
                 int64_t S, int64_t D, const lcv_bsa_strides& qs, const lcv_bsa_strides& ks,
                 const lcv_bsa_strides& vs, int64_t top_k, float sm_scale, const lcv_bsa_geom& g,
-                int64_t nb, int64_t bs, float* qbar, float* kbar, float* score, int32_t* order,
-                int32_t* idx, void* out, const lcv_bsa_strides& os, hipStream_t s,
+                int64_t nb, int64_t bs, float* qbar, float* kbar, float* score, int64_t score_bh,
+                int32_t* order, int32_t* idx, void* out, const lcv_bsa_strides& os, hipStream_t s,
                 const char* name) {
   char what[96];
   const lcv::Tensor4 ts[2] = {{q, qs.b, qs.h, qs.s}, {k, ks.b, ks.h, ks.s}};
@@ -362,15 +364,21 @@ int run_forward(const void* q, const void* k, const void* v, int dtype, int64_t 
                          what);
   if (st) return st;
   if (score) {
-    snprintf(what, sizeof(what), "%s(scores)", name);
-    st = launch_status(lcv::launch_scores(qbar, kbar, (int)B, (int)H, (int)nb, (int)nb, (int)D,
-                                          score, s),
-                       what);
-    if (st) return st;
-    snprintf(what, sizeof(what), "%s(top-k)", name);
-    st = launch_status(lcv::launch_topk(score, (int)B, (int)H, (int)nb, (int)nb, (int)top_k, idx,
-                                        s),
-                       what);
+    // Slices [c0, c0 + n) of the B*H (b, h) pairs; the scores of one slice
+    // are read by its top-k before the next slice's GEMM rewrites them (one
+    // stream).
+    for (int64_t c0 = 0; c0 < B * H && !st; c0 += score_bh) {
+      const int64_t n = B * H - c0 < score_bh ? B * H - c0 : score_bh;
+      snprintf(what, sizeof(what), "%s(scores)", name);
+      st = launch_status(lcv::launch_scores(qbar + c0 * nb * D, kbar + c0 * nb * D, 1, (int)n,
+                                            (int)nb, (int)nb, (int)D, score, s),
+                         what);
+      if (st) return st;
+      snprintf(what, sizeof(what), "%s(top-k)", name);
+      st = launch_status(lcv::launch_topk(score, 1, (int)n, (int)nb, (int)nb, (int)top_k,
+                                          idx + c0 * nb * top_k, s),
+                         what);
+    }
   } else {
     snprintf(what, sizeof(what), "%s(select)", name);
     st = launch_status(lcv::launch_select(qbar, kbar, (int)B, (int)H, (int)nb, (int)nb, (int)D,
@@ -404,6 +412,10 @@ int run_forward(const void* q, const void* k, const void* v, int dtype, int64_t 
 constexpr size_t kNoAllocScratchBytes = size_t{64} << 20;  // LCV_BSA_NOALLOC_SCRATCH_BYTES
 static_assert(kNoAllocScratchBytes == LCV_BSA_NOALLOC_SCRATCH_BYTES, "header and library agree");
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+// At most this many score slices (two launches each) in the no-allocation
+// routing; beyond it the single fused select launch is the faster route.
+constexpr int64_t kMaxScoreSlices = 8;
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
@@ -454,7 +466,7 @@ int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype, int6
   char* ws = reinterpret_cast<char*>(workspace);
   return run_forward(q, k, v, dtype, B, H, S, D, qs, ks, vs, top_k, sm_scale, g, nb, bs,
                      reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws + pb),
-                     reinterpret_cast<float*>(ws + 2 * pb),
+                     reinterpret_cast<float*>(ws + 2 * pb), B * H,
                      reinterpret_cast<int32_t*>(ws + 2 * pb + score_bytes(B, H, nb)), idx, out, os,
                      (hipStream_t)stream, "lcv_bsa_forward");
 }
@@ -478,11 +490,19 @@ int lcv_bsa_forward_noalloc(const void* q, const void* k, const void* v, int dty
                 "bytes; call lcv_bsa_forward with a workspace instead",
                 (long long)B, (long long)H, (long long)nb, (long long)D, need,
                 kNoAllocScratchBytes);
+  // The scratch left after the means and the launch order holds the block
+  // scores of score_bh (b, h) slices; the two-kernel routing runs slice by
+  // slice when a few slices cover every head (at 720p, H=32: 11 heads a
+  // slice, 3 slices), else the fused select kernel routes without scores.
+  const size_t slice = align256((size_t)nb * nb * sizeof(float));
+  const int64_t score_bh = (int64_t)((kNoAllocScratchBytes - need) / slice);
+  const bool sliced = score_bh > 0 && (B * H + score_bh - 1) / score_bh <= kMaxScoreSlices;
   void* base = nullptr;
   if ((st = scratch_on_current_device(&base))) return st;
   char* ws = reinterpret_cast<char*>(base);
   return run_forward(q, k, v, dtype, B, H, S, D, qs, ks, vs, top_k, sm_scale, g, nb, bs,
-                     reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws + pb), nullptr,
+                     reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws + pb),
+                     sliced ? reinterpret_cast<float*>(ws + need) : nullptr, score_bh,
                      reinterpret_cast<int32_t*>(ws + 2 * pb), idx, out, os, (hipStream_t)stream,
                      "lcv_bsa_forward_noalloc");
 }

@@ -75,3 +75,12 @@ def test_noalloc_refuses_beyond_scratch(device):
     st = _call(lib, "lcv_bsa_forward_noalloc", q, q, q, top_k, (1, 1, S), (1, 1, 64), out, idx)
     assert st == _lib.ERR_UNSUPPORTED
     assert b"fixed device scratch" in lib.lcv_bsa_last_error()
+
+
+def test_noalloc_fused_route_when_score_slices_do_not_fit(device):
+    """56 heads at 720p leave scratch for 4 heads of block scores: 14 slices,
+    more than the sliced route takes, so the fused select kernel routes."""
+    from lcv_bsa import _lib
+
+    lib = _lib.load()
+    _compare(device, lib, 1, 56, (16, 45, 80), 128, torch.float16, 57, seed=33)
