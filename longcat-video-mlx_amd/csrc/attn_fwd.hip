@@ -10,10 +10,11 @@
 // longcat_video/models/block_sparse_attention_metal.py:75-164, 572-712, 829-962)
 // gives the same result.
 //
-// MFMA kernel (fp16 / bf16, D in {64, 128}, sm_scale >= 0):
+// MFMA kernels (fp16 / bf16, sm_scale >= 0): attn_half_kernel for D = 128
+// and attn_mfma_kernel for D = 64.  attn_mfma_kernel:
 //   * one workgroup (2 waves) per (b, h, q-block); wave w owns query rows
-//     32w..32w+31 of the block; two waves per SIMD are resident (register
-//     budget 256), so one wave's softmax overlaps the other's MFMAs;
+//     32w..32w+31 of the block; several waves per SIMD are resident, so one
+//     wave's softmax overlaps another's MFMAs;
 //   * the wave's Q tile stays in registers as the B operand of
 //     S^T = K Q^T (v_mfma_f32_32x32x16_{f16,bf16}, fp32 accumulate);
 //   * S^T's accumulator layout (lane = query column; runs of 4 consecutive
@@ -42,6 +43,11 @@
 //   * the routing list is read 64 entries at a time; each lane turns its entry
 //     into the block's first token once, so a tile costs one v_readlane;
 //   * the output tile is staged through LDS and written as whole rows.
+//
+// attn_half_kernel keeps that work unit, layout and walk but processes each
+// 64-key block as two 32-key halves, whose K and V half tiles stream through
+// a three-slot LDS ring; its smaller state fits three waves per SIMD at
+// D = 128 (see its own comment).
 //
 // Vector-ALU kernel (any dtype, D in {16, 32, 64, 128, 256}, any scale): 64
 // rows x 4 lanes per workgroup, fp32 throughout; used for fp32 inputs, head
@@ -237,10 +243,11 @@ struct MfmaCfg {
   __device__ static int vswz(int r) { return 4 * ((r / RP) % (DC / 4)); }
 };
 
-// Waves per SIMD the register allocation must allow.  D = 128 uses the
-// 256-register budget of two waves.  D = 64 holds three (132 registers; its
-// 16 KB of LDS per workgroup would allow eight workgroups per CU): asking
-// for four makes the allocator spill to scratch.
+// Waves per SIMD the register allocation must allow.  D = 64 holds three
+// (132 registers; its 16 KB of LDS per workgroup would allow eight
+// workgroups per CU): asking for four makes the allocator spill to scratch.
+// (D = 128 runs in attn_half_kernel; this kernel at D = 128 needs the
+// 256-register budget of two waves.)
 template <int D>
 struct MfmaOccupancy {
   static constexpr int kWaves = D == 128 ? 2 : 3;
@@ -575,6 +582,324 @@ void attn_mfma_kernel(AttnParams p) {
 
 
 // ---------------------------------------------------------------------------
+// Half-block MFMA kernel (fp16 / bf16, D = 128), three waves per SIMD.  The
+// work unit of attn_mfma_kernel (one workgroup of 2 waves per (b, h,
+// q-block), wave w owns query rows 32w .. 32w + 31), but each listed
+// 64-key block is processed as two 32-key halves, one after the other: S^T
+// of a half is one 32 x 32 MFMA tile (16 registers), its P half of that, so
+// a wave fits in 168 registers, and the K and V half tiles (8 KB each) flow
+// through a ring of three 8 KB LDS slots, 24 KB per workgroup: six
+// workgroups per CU.
+//
+// Ring order, per block: K(lo), V(lo), K(hi), V(hi).  Element e of that
+// sequence sits in slot e mod 3.  At the barrier that starts element e,
+// both waves have consumed element e - 1 and waited for their halves of e,
+// so the DMA of element e + 2 goes into e - 1's slot: every half tile is
+// fetched two elements ahead.  One barrier per element, four per block, as
+// in attn_mfma_kernel.  The online softmax runs per half: the first half's
+// row max sets the exponent offset, and each half has its own 2^15 check and
+// redo.  Only the rounding of the sums differs from whole-block processing.
+// The launch slots rotate the walk as in attn_mfma_kernel, over the 192
+// workgroups resident per XCD.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 3)))
+void attn_half_kernel(AttnParams p) {
+  constexpr int D = 128;
+  typedef MfmaCfg<T, D> C;
+  typedef typename Mfma<T>::vec8 vec8;
+  constexpr int kSlotBytes = 32 * 2 * D;  // 8 KB: 32 rows of K or V
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[3 * kSlotBytes];
+
+  const int wid = xcd_linear_work_id(blockIdx.x, gridDim.x);
+  const int bh = wid / p.nb;
+  const int qb = p.order ? uniform_i32(p.order[wid]) : wid - bh * p.nb;
+  if ((uint32_t)qb >= (uint32_t)p.nb) return;  // a launch-order entry outside [0, nb): nothing to do
+  const int b = bh / p.H;
+  const int h = bh - b * p.H;
+  const int tid = threadIdx.x;
+  const int wave = uniform_i32(tid / 64);
+  const int lane = tid % 64;
+  const int l32 = lane % 32;
+  const int g = lane / 32;
+
+  const T* qbase = reinterpret_cast<const T*>(p.q) + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
+  const T* kbase = reinterpret_cast<const T*>(p.k) + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
+  const T* vbase = reinterpret_cast<const T*>(p.v) + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
+  T* obase = reinterpret_cast<T*>(p.out) + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh;
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, (int)p.k_head_bytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, (int)p.v_head_bytes, kBufferFlags);
+
+  TileList list(p.idx + ((int64_t)bh * p.nb + qb) * p.top_k, p.top_k, p.nk);
+
+  const int32_t qtok = block_base_token(p.g, qb) + voxel_row_offset(p.g, 32 * wave + l32);
+  vec8 qf[D / 16];
+  {
+    const T* qrow = qbase + (int64_t)qtok * p.q_ss + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+      qf[ks] = __builtin_bit_cast(vec8, *reinterpret_cast<const u32x4*>(qrow + 16 * ks));
+  }
+  list.finish(p.gk);
+
+  // ---- DMA: a half tile is 32 rows (8 KB, 8 wave loads of 4 rows); wave w
+  // loads rows 16w .. 16w + 15 of it (4 loads).  Row r + 32 of a block sits
+  // voxel_row_offset(32) tokens after row r (voxel sides are powers of two),
+  // so the high half uses the low half's lane offsets plus a scalar.
+  uint32_t kvo[4], vvo[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = 4 * wave + u;                   // 1 KB load index within the half tile
+    const int row = t * C::kRowsPerDma + lane / C::DC;  // 0 .. 31
+    const int pc = lane % C::DC;
+    const uint32_t tokoff = (uint32_t)voxel_row_offset(p.gk, row);
+    kvo[u] = (tokoff * (uint32_t)p.k_ss + 8u * (pc ^ C::kswz(row))) * sizeof(T) - 1024u * u;
+    vvo[u] = (tokoff * (uint32_t)p.v_ss + 8u * (pc ^ C::vswz(row))) * sizeof(T) - 1024u * u;
+  }
+  const uint32_t k_row_bytes = (uint32_t)p.k_ss * sizeof(T);
+  const uint32_t v_row_bytes = (uint32_t)p.v_ss * sizeof(T);
+  const uint32_t hi_tok = (uint32_t)voxel_row_offset(p.gk, 32);
+  // Element e = 4 (block) + 2 (half) + (0: K, 1: V) into slot `slot`.
+  auto dma = [&](int32_t tok, int half, int isv, int slot) {
+    const uint32_t t = (uint32_t)tok + (half ? hi_tok : 0u);
+    const uint32_t m0v = lds_addr(ring + slot * kSlotBytes + 1024 * (4 * wave));
+    if (isv) {
+      const int off = (int)(t * v_row_bytes);
+      dma16<0>(vrs, vvo[0], off, m0v);
+      dma16<1024>(vrs, vvo[1], off, m0v);
+      dma16<2048>(vrs, vvo[2], off, m0v);
+      dma16<3072>(vrs, vvo[3], off, m0v);
+    } else {
+      const int off = (int)(t * k_row_bytes);
+      dma16<0>(krs, kvo[0], off, m0v);
+      dma16<1024>(krs, kvo[1], off, m0v);
+      dma16<2048>(krs, kvo[2], off, m0v);
+      dma16<3072>(krs, kvo[3], off, m0v);
+    }
+  };
+
+  const int kaddr = l32 * (2 * D);
+  const int ksw0 = C::kswz(l32);
+  const int G = lane / 16, gi = lane % 16;
+  const int vrow0 = 4 * g + gi / 4;
+  const int vcol0 = 16 * (G % 2) + 4 * (gi % 4);
+
+  f32x16 oacc[D / 32];
+#pragma unroll
+  for (int md = 0; md < D / 32; ++md)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) oacc[md][i] = 0.0f;
+  float m_run = 0.0f;
+  float l_run = 0.0f;
+  bool first = true;
+  const float sl2 = p.scale_log2;
+
+  constexpr int kResident = 192;  // workgroups resident per XCD (32 CUs x 6)
+  const int slot0 = blockIdx.x / kNumXcd;
+  const int n0 = (int)(((int64_t)(slot0 % kResident) * p.nk) / kResident);
+  const int j0 = list.count_below(n0, p.gk);
+  const bool one_chunk = p.top_k <= 64;
+  const int r0 = j0 & 63;
+  uint64_t rem = 0;
+  if (one_chunk) {
+    const uint64_t v = list.valid;
+    rem = r0 == 0 ? v : (v >> r0) | (v << (64 - r0));
+  }
+  auto next_rot = [&](int j) -> int {
+    if (one_chunk) {
+      if (rem == 0) return p.top_k;
+      const int bb = (int)__builtin_ctzll(rem);
+      rem &= rem - 1;
+      return (bb + r0) & 63;
+    }
+    if (j < 0 || j >= j0) {
+      const int r = list.next(j < 0 ? j0 : j + 1, p.gk);
+      if (r < p.top_k) return r;
+      j = -1;
+    }
+    const int r = list.next(j + 1, p.gk);
+    return r < j0 ? r : p.top_k;
+  };
+
+  int j = next_rot(-1);
+  int32_t tok = j < p.top_k ? list.token(j) : 0;
+  // Elements 0 and 1 of the ring: K(lo), V(lo) of the first block.
+  if (j < p.top_k) {
+    dma(tok, 0, 0, 0);
+    dma(tok, 0, 1, 1);
+  }
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) asm volatile("" ::"v"(qf[ks]));
+
+  int s_cur = 0;  // slot of the element being started
+  vec8 pf[2];     // P^T of the current half: key steps s = 0, 1
+  f32x16 sacc;
+  while (j < p.top_k) {
+    const int jn = next_rot(j);
+    const bool more = jn < p.top_k;
+    const int32_t tokn = more ? list.token(jn) : 0;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      // ===== K half: S^T (32 keys x 32 queries) = K Q^T, then P.
+      wait_vmcnt<4>();  // this element landed; the next one may be in flight
+      __syncthreads();  // both halves landed; the slot of the previous element is free
+      {
+        const int s_free = s_cur == 0 ? 2 : s_cur - 1;
+        // Element + 2: K(hi) of this block after K(lo); K(lo) of the next block after K(hi).
+        if (half == 0) dma(tok, 1, 0, s_free);
+        else if (more) dma(tokn, 0, 0, s_free);
+      }
+      const uint8_t* Ks = ring + s_cur * kSlotBytes;
+      s_cur = s_cur == 2 ? 0 : s_cur + 1;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sacc[i] = 0.0f;
+      {
+        constexpr int kSteps = D / 16;
+        constexpr int kPf = 3;
+        vec8 kf[kSteps];
+        auto read_k = [&](int ks) {
+          kf[ks] = __builtin_bit_cast(
+              vec8, *reinterpret_cast<const u32x4*>(Ks + kaddr + 16 * ((2 * ks + g) ^ ksw0)));
+        };
+#pragma unroll
+        for (int ks = 0; ks < kPf; ++ks) read_k(ks);
+        __builtin_amdgcn_sched_group_barrier(0x100, kPf, 0);
+#pragma unroll
+        for (int ks = 0; ks < kSteps; ++ks) {
+          if (ks + kPf < kSteps) read_k(ks + kPf);
+          sacc = Mfma<T>::mma(kf[ks], qf[ks], sacc);
+          if (ks + kPf < kSteps) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+      }
+      auto rowmax = [&]() {
+        float mx = fmax3(sacc[0], sacc[1], sacc[2]);
+#pragma unroll
+        for (int i = 3; i < 15; i += 2) mx = fmax3(mx, sacc[i], sacc[i + 1]);
+        mx = fmax3(mx, sacc[15], sacc[15]);
+        return max_halves(mx) * sl2;
+      };
+      auto exps = [&]() {
+        float ls[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj)
+            pf[s][jj] = from_f32<T>(fast_exp2(fmaf(sacc[8 * s + jj], sl2, -m_run)));
+          ls[s] = Mfma<T>::sum8(pf[s], 0.0f);
+        }
+        return ls[0] + ls[1];
+      };
+      if (first) m_run = rowmax();
+      float ls = exps();
+      if (__ballot(!(ls <= kMaxTileSum))) {  // wave-uniform, rare
+        const float m_new = fmax3(m_run, rowmax(), m_run);
+        const float corr = fast_exp2(m_run - m_new);
+        l_run *= corr;
+#pragma unroll
+        for (int md = 0; md < D / 32; ++md)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[md][i] *= corr;
+        m_run = m_new;
+        ls = exps();
+      }
+      l_run += ls;
+      first = false;
+
+      // ===== V half: O^T += V^T P^T over its 32 keys.
+      // In flight: this V [, the element after it].  The last element of the
+      // last block has nothing behind it.
+      if (half == 1 && !more)
+        wait_vmcnt<0>();
+      else
+        wait_vmcnt<4>();
+      __syncthreads();
+      {
+        const int s_free = s_cur == 0 ? 2 : s_cur - 1;
+        // Element + 2: V(hi) of this block after V(lo); V(lo) of the next after V(hi).
+        if (half == 0) dma(tok, 1, 1, s_free);
+        else if (more) dma(tokn, 0, 1, s_free);
+      }
+      const uint8_t* Vs = ring + s_cur * kSlotBytes;
+      s_cur = s_cur == 2 ? 0 : s_cur + 1;
+      {
+        vec8 vf[2][D / 32];
+        auto read_v = [&](int s, vec8* dst) {
+#pragma unroll
+          for (int md = 0; md < D / 32; ++md) {
+            v4s half_lo, half_hi;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              const int row = 16 * s + 8 * hh + vrow0;
+              const int col = 32 * md + vcol0;
+              const int addr = row * (2 * D) + 16 * ((col / 8) ^ C::vswz(row)) + 2 * (col % 8);
+              const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(Vs + addr));
+              if (hh == 0) half_lo = r; else half_hi = r;
+            }
+            dst[md] = __builtin_bit_cast(
+                vec8, (short __attribute__((ext_vector_type(8)))){half_lo[0], half_lo[1], half_lo[2],
+                                                                  half_lo[3], half_hi[0], half_hi[1],
+                                                                  half_hi[2], half_hi[3]});
+          }
+        };
+        read_v(0, vf[0]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * (D / 32), 0);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          if (s + 1 < 2) read_v(s + 1, vf[1]);
+#pragma unroll
+          for (int md = 0; md < D / 32; ++md) {
+            oacc[md] = Mfma<T>::mma(vf[s][md], pf[s], oacc[md]);
+            if (s + 1 < 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          }
+        }
+      }
+    }
+    j = jn;
+    tok = tokn;
+  }
+
+  // ---- Normalise, stage the 64 x D output tile in the ring (slots 0-1),
+  // write whole rows.
+  const float l_tot = sum_halves(l_run);
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  __syncthreads();  // every ring read done (no DMA is outstanding here)
+  {
+    const int row = 32 * wave + l32;
+    uint8_t* orow = ring + row * (2 * D);
+#pragma unroll
+    for (int md = 0; md < D / 32; ++md) {
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        u32x2 w;
+        w[0] = bits16(from_f32<T>(oacc[md][4 * i4 + 0] * inv)) |
+               (bits16(from_f32<T>(oacc[md][4 * i4 + 1] * inv)) << 16);
+        w[1] = bits16(from_f32<T>(oacc[md][4 * i4 + 2] * inv)) |
+               (bits16(from_f32<T>(oacc[md][4 * i4 + 3] * inv)) << 16);
+        const int chunk = 4 * md + i4;
+        *reinterpret_cast<u32x2*>(orow + 16 * (chunk ^ C::kswz(row)) + 8 * g) = w;
+      }
+    }
+  }
+  __syncthreads();
+  {
+    const int32_t tok0 = block_base_token(p.g, qb);
+#pragma unroll
+    for (int u = 0; u < 64 * C::DC / C::kThreads; ++u) {
+      const int pidx = tid + C::kThreads * u;
+      const int row = pidx / C::DC;
+      const int c = pidx % C::DC;
+      const int32_t t = tok0 + voxel_row_offset(p.g, row);
+      *reinterpret_cast<u32x4*>(obase + (int64_t)t * p.o_ss + 8 * c) =
+          *reinterpret_cast<const u32x4*>(ring + row * (2 * D) + 16 * (c ^ C::kswz(row)));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Vector-ALU kernel: workgroup = 64 query rows x 4 lanes; lane (r, quarter)
 // owns D/4 columns of q and o.  K/V are staged 32 keys at a time as fp32.
 // ---------------------------------------------------------------------------
@@ -662,7 +987,10 @@ __global__ __launch_bounds__(256) void attn_valu_kernel(AttnParams p) {
 template <typename T, int D>
 hipError_t launch_mfma(const AttnParams& p, hipStream_t stream) {
   const int grid = p.B * p.H * p.nb;
-  hipLaunchKernelGGL((attn_mfma_kernel<T, D>), dim3(grid), dim3(128), 0, stream, p);
+  if constexpr (D == 128)
+    hipLaunchKernelGGL((attn_half_kernel<T>), dim3(grid), dim3(128), 0, stream, p);
+  else
+    hipLaunchKernelGGL((attn_mfma_kernel<T, D>), dim3(grid), dim3(128), 0, stream, p);
   return hipGetLastError();
 }
 
