@@ -602,6 +602,11 @@ void attn_mfma_kernel(AttnParams p) {
 // The launch slots rotate the walk as in attn_mfma_kernel, over the 192
 // workgroups resident per XCD.
 // ---------------------------------------------------------------------------
+template <int N>
+struct Phase {
+  static constexpr int value = N;
+};
+
 template <typename T>
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 3)))
 void attn_half_kernel(AttnParams p) {
@@ -733,10 +738,14 @@ void attn_half_kernel(AttnParams p) {
 #pragma unroll
   for (int ks = 0; ks < D / 16; ++ks) asm volatile("" ::"v"(qf[ks]));
 
-  int s_cur = 0;  // slot of the element being started
-  vec8 pf[2];     // P^T of the current half: key steps s = 0, 1
+  vec8 pf[2];  // P^T of the current half: key steps s = 0, 1
   f32x16 sacc;
-  while (j < p.top_k) {
+  // One listed block.  Its elements are 4 (position in the walk) + t, so
+  // with PH = position mod 3 element t sits in slot (PH + t) mod 3 and the
+  // slot it frees for element t + 2 is (PH + t + 2) mod 3: with the walk
+  // unrolled three blocks deep, every slot address is a constant.
+  auto run_block = [&](auto phase) {
+    constexpr int PH = decltype(phase)::value;
     const int jn = next_rot(j);
     const bool more = jn < p.top_k;
     const int32_t tokn = more ? list.token(jn) : 0;
@@ -746,13 +755,12 @@ void attn_half_kernel(AttnParams p) {
       wait_vmcnt<4>();  // this element landed; the next one may be in flight
       __syncthreads();  // both halves landed; the slot of the previous element is free
       {
-        const int s_free = s_cur == 0 ? 2 : s_cur - 1;
         // Element + 2: K(hi) of this block after K(lo); K(lo) of the next block after K(hi).
-        if (half == 0) dma(tok, 1, 0, s_free);
-        else if (more) dma(tokn, 0, 0, s_free);
+        const int t = 2 * half;
+        if (half == 0) dma(tok, 1, 0, (PH + t + 2) % 3);
+        else if (more) dma(tokn, 0, 0, (PH + t + 2) % 3);
       }
-      const uint8_t* Ks = ring + s_cur * kSlotBytes;
-      s_cur = s_cur == 2 ? 0 : s_cur + 1;
+      const uint8_t* Ks = ring + ((PH + 2 * half) % 3) * kSlotBytes;
 #pragma unroll
       for (int i = 0; i < 16; ++i) sacc[i] = 0.0f;
       {
@@ -817,13 +825,12 @@ void attn_half_kernel(AttnParams p) {
         wait_vmcnt<4>();
       __syncthreads();
       {
-        const int s_free = s_cur == 0 ? 2 : s_cur - 1;
         // Element + 2: V(hi) of this block after V(lo); V(lo) of the next after V(hi).
-        if (half == 0) dma(tok, 1, 1, s_free);
-        else if (more) dma(tokn, 0, 1, s_free);
+        const int t = 2 * half + 1;
+        if (half == 0) dma(tok, 1, 1, (PH + t + 2) % 3);
+        else if (more) dma(tokn, 0, 1, (PH + t + 2) % 3);
       }
-      const uint8_t* Vs = ring + s_cur * kSlotBytes;
-      s_cur = s_cur == 2 ? 0 : s_cur + 1;
+      const uint8_t* Vs = ring + ((PH + 2 * half + 1) % 3) * kSlotBytes;
       {
         vec8 vf[2][D / 32];
         auto read_v = [&](int s, vec8* dst) {
@@ -860,6 +867,13 @@ void attn_half_kernel(AttnParams p) {
     }
     j = jn;
     tok = tokn;
+  };
+  while (j < p.top_k) {
+    run_block(Phase<0>{});
+    if (j >= p.top_k) break;
+    run_block(Phase<1>{});
+    if (j >= p.top_k) break;
+    run_block(Phase<2>{});
   }
 
   // ---- Normalise, stage the 64 x D output tile in the ring (slots 0-1),
