@@ -44,10 +44,12 @@
 //     into the block's first token once, so a tile costs one v_readlane;
 //   * the output tile is staged through LDS and written as whole rows.
 //
-// attn_half_kernel keeps that work unit, layout and walk but processes each
-// 64-key block as two 32-key halves, whose K and V half tiles stream through
-// a three-slot LDS ring; its smaller state fits three waves per SIMD at
-// D = 128 (see its own comment).
+// attn_half_kernel keeps that work unit, swizzled DMA and walk but processes
+// each 64-key block as two 32-key halves on 16 x 16 x 32 MFMAs, whose K and
+// V half tiles stream through a three-slot LDS ring; its smaller state fits
+// three waves per SIMD at D = 128.  Its offset guard differs: a wave whose
+// tile sum passes 2^15 does not rescale O in place; the workgroup finds the
+// exact row maxima and walks its list again (see its own comment).
 //
 // Vector-ALU kernel (any dtype, D in {16, 32, 64, 128, 256}, any scale): 64
 // rows x 4 lanes per workgroup, fp32 throughout; used for fp32 inputs, head
@@ -57,8 +59,10 @@
 namespace lcv {
 namespace {
 
-// MFMA kernel: a tile is redone against a raised offset when the partial sum
-// of its P values exceeds this (so every P <= 2^15, a normal fp16 value).
+// MFMA kernels: bound on a tile's partial sum of P values, so that every P
+// stays <= 2^15, a normal fp16 value.  Past it attn_mfma_kernel redoes the
+// tile against a raised offset and attn_half_kernel walks again with the
+// exact row maxima.
 constexpr float kMaxTileSum = 32768.0f;
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit dwords (gfx9 family)
 
@@ -584,28 +588,75 @@ void attn_mfma_kernel(AttnParams p) {
 // ---------------------------------------------------------------------------
 // Half-block MFMA kernel (fp16 / bf16, D = 128), three waves per SIMD.  The
 // work unit of attn_mfma_kernel (one workgroup of 2 waves per (b, h,
-// q-block), wave w owns query rows 32w .. 32w + 31), but each listed
-// 64-key block is processed as two 32-key halves, one after the other: S^T
-// of a half is one 32 x 32 MFMA tile (16 registers), its P half of that, so
-// a wave fits in 168 registers, and the K and V half tiles (8 KB each) flow
-// through a ring of three 8 KB LDS slots, 24 KB per workgroup: six
-// workgroups per CU.
+// q-block), wave w owns query rows 32w .. 32w + 31), but each listed 64-key
+// block is processed as two 32-key halves, one after the other, and both
+// products run on 16 x 16 x 32 MFMAs.  Per wave and half:
+//   S^T[kt][qt] (16 keys x 16 queries) += K[kt] (16 x 32 of D) Q^T[qt] over
+//     4 D steps: 16 MFMAs; lane l holds query 16 qt + l % 16 and keys
+//     16 kt + 4 (l / 16) + i;
+//   O^T[dt][qt] (16 of D x 16 queries) += V^T[dt] (16 x 32 keys) P^T[qt]:
+//     16 MFMAs.  P^T stays in registers as the B operand: its contraction
+//     index 8 (l / 16) + j stands for key 16 (j / 4) + 4 (l / 16) + j % 4,
+//     and the V^T operand is read from LDS in the same key order.
+// The 16 x 16 form reads a fifth fewer operand registers per FLOP than
+// 32 x 32 x 16, and on this power-limited chip that is time.  Each query's
+// keys sit in four lane groups (l, l ^ 16, l ^ 32, l ^ 48): the row max and
+// the final row sum reduce over all four (v_permlane16_swap, then
+// v_permlane32_swap).  A wave's state (Q 32, O 64, S 16, P 8 registers) fits
+// 168 registers.
 //
-// Ring order, per block: K(lo), V(lo), K(hi), V(hi).  Element e of that
-// sequence sits in slot e mod 3.  At the barrier that starts element e,
-// both waves have consumed element e - 1 and waited for their halves of e,
-// so the DMA of element e + 2 goes into e - 1's slot: every half tile is
-// fetched two elements ahead.  One barrier per element, four per block, as
-// in attn_mfma_kernel.  The online softmax runs per half: the first half's
-// row max sets the exponent offset, and each half has its own 2^15 check and
-// redo.  Only the rounding of the sums differs from whole-block processing.
-// The launch slots rotate the walk as in attn_mfma_kernel, over the 192
-// workgroups resident per XCD.
+// The K and V half tiles (8 KB each) flow through a ring of three 8 KB LDS
+// slots, 24 KB per workgroup: six workgroups per CU.  Ring order, per block:
+// K(lo), V(lo), K(hi), V(hi).  Element e of that sequence sits in slot
+// e mod 3.  At the barrier that starts element e, both waves have consumed
+// element e - 1 and waited for their halves of e, so the DMA of element
+// e + 2 goes into e - 1's slot: every half tile is fetched two elements
+// ahead, with one barrier per element.  K rows keep the whole-block
+// kernel's swizzle; V rows are swizzled so that the 32 lanes of a
+// transposing read (8 rows x 32 bytes) hit distinct banks: chunk c of row r
+// sits at c ^ (2 (r mod 8)).  The launch slots rotate the walk as in
+// attn_mfma_kernel, over the 192 workgroups resident per XCD.
 // ---------------------------------------------------------------------------
 template <int N>
 struct Phase {
   static constexpr int value = N;
 };
+
+template <typename T>
+struct Mfma16;
+
+template <>
+struct Mfma16<f16> {
+  __device__ static f32x4 mma(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma16<bf16> {
+  __device__ static f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Lanes l and l ^ 16 exchange x through v_permlane16_swap; the two results
+// hold x[l] and x[l ^ 16] in some order.
+__device__ __forceinline__ void swap_rows16(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x),
+                                                  __builtin_bit_cast(uint32_t, x), false, false);
+  a = __builtin_bit_cast(float, (uint32_t)r[0]);
+  b = __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+__device__ __forceinline__ float max_quarters(float x) {
+  float a, b;
+  swap_rows16(x, a, b);
+  return max_halves(__builtin_elementwise_maximum(a, b));
+}
+__device__ __forceinline__ float sum_quarters(float x) {
+  float a, b;
+  swap_rows16(x, a, b);
+  return sum_halves(a + b);
+}
 
 template <typename T>
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 3)))
@@ -625,8 +676,8 @@ void attn_half_kernel(AttnParams p) {
   const int tid = threadIdx.x;
   const int wave = uniform_i32(tid / 64);
   const int lane = tid % 64;
-  const int l32 = lane % 32;
-  const int g = lane / 32;
+  const int G = lane / 16;   // lane group: keys 4G.. of each 16-key tile, D rows 4G.. of O
+  const int gi = lane % 16;  // query 16 qt + gi
 
   const T* qbase = reinterpret_cast<const T*>(p.q) + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
   const T* kbase = reinterpret_cast<const T*>(p.k) + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
@@ -639,13 +690,15 @@ void attn_half_kernel(AttnParams p) {
 
   TileList list(p.idx + ((int64_t)bh * p.nb + qb) * p.top_k, p.top_k, p.nk);
 
-  const int32_t qtok = block_base_token(p.g, qb) + voxel_row_offset(p.g, 32 * wave + l32);
-  vec8 qf[D / 16];
-  {
-    const T* qrow = qbase + (int64_t)qtok * p.q_ss + 8 * g;
+  // Q^T operand: qf[qt][ks] holds query 32 wave + 16 qt + gi, D 32 ks + 8 G .. + 7.
+  vec8 qf[2][D / 32];
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
-      qf[ks] = __builtin_bit_cast(vec8, *reinterpret_cast<const u32x4*>(qrow + 16 * ks));
+  for (int qt = 0; qt < 2; ++qt) {
+    const int32_t qtok = block_base_token(p.g, qb) + voxel_row_offset(p.g, 32 * wave + 16 * qt + gi);
+    const T* qrow = qbase + (int64_t)qtok * p.q_ss + 8 * G;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks)
+      qf[qt][ks] = __builtin_bit_cast(vec8, *reinterpret_cast<const u32x4*>(qrow + 32 * ks));
   }
   list.finish(p.gk);
 
@@ -653,20 +706,20 @@ void attn_half_kernel(AttnParams p) {
   // loads rows 16w .. 16w + 15 of it (4 loads).  Row r + 32 of a block sits
   // voxel_row_offset(32) tokens after row r (voxel sides are powers of two),
   // so the high half uses the low half's lane offsets plus a scalar.
+  auto vswz16 = [](int r) { return 2 * (r % 8); };
   uint32_t kvo[4], vvo[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int t = 4 * wave + u;                   // 1 KB load index within the half tile
+    const int t = 4 * wave + u;
     const int row = t * C::kRowsPerDma + lane / C::DC;  // 0 .. 31
     const int pc = lane % C::DC;
     const uint32_t tokoff = (uint32_t)voxel_row_offset(p.gk, row);
     kvo[u] = (tokoff * (uint32_t)p.k_ss + 8u * (pc ^ C::kswz(row))) * sizeof(T) - 1024u * u;
-    vvo[u] = (tokoff * (uint32_t)p.v_ss + 8u * (pc ^ C::vswz(row))) * sizeof(T) - 1024u * u;
+    vvo[u] = (tokoff * (uint32_t)p.v_ss + 8u * (pc ^ vswz16(row))) * sizeof(T) - 1024u * u;
   }
   const uint32_t k_row_bytes = (uint32_t)p.k_ss * sizeof(T);
   const uint32_t v_row_bytes = (uint32_t)p.v_ss * sizeof(T);
   const uint32_t hi_tok = (uint32_t)voxel_row_offset(p.gk, 32);
-  // Element e = 4 (block) + 2 (half) + (0: K, 1: V) into slot `slot`.
   auto dma = [&](int32_t tok, int half, int isv, int slot) {
     const uint32_t t = (uint32_t)tok + (half ? hi_tok : 0u);
     const uint32_t m0v = lds_addr(ring + slot * kSlotBytes + 1024 * (4 * wave));
@@ -685,19 +738,31 @@ void attn_half_kernel(AttnParams p) {
     }
   };
 
-  const int kaddr = l32 * (2 * D);
-  const int ksw0 = C::kswz(l32);
-  const int G = lane / 16, gi = lane % 16;
-  const int vrow0 = 4 * g + gi / 4;
-  const int vcol0 = 16 * (G % 2) + 4 * (gi % 4);
+  // LDS operand addresses.  K[kt] for D step ks: row 16 kt + gi (kt adds
+  // 4 KB), chunk 4 ks + G.  V^T[dt]: rows 4 G .. 4 G + 3 (+ 16 for the
+  // second key group, 4 KB further), columns 16 dt + 4 (gi % 4) .. + 3.
+  // The swizzles XOR bit fields that nothing else in the address uses, so
+  // the address of step ks (dt) is that of step 0 with 64 ks (32 dt) XORed in.
+  int kaddr[D / 32];
+#pragma unroll
+  for (int ks = 0; ks < D / 32; ++ks) kaddr[ks] = gi * (2 * D) + 16 * ((4 * ks + G) ^ C::kswz(gi));
+  const int vrow = 4 * G + gi / 4;
+  const int vaddr0 = vrow * (2 * D) + 16 * (((4 * (gi % 4)) / 8) ^ vswz16(vrow)) + 2 * ((4 * (gi % 4)) % 8);
+  auto vaddr = [&](int dt) { return vaddr0 ^ (32 * dt); };
 
-  f32x16 oacc[D / 32];
+  typedef f32x4 OTiles[D / 16][2];  // O^T tile (dt, qt)
+  auto zero_o = [](OTiles& o) {
 #pragma unroll
-  for (int md = 0; md < D / 32; ++md)
+    for (int dt = 0; dt < D / 16; ++dt)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) oacc[md][i] = 0.0f;
-  float m_run = 0.0f;
-  float l_run = 0.0f;
+      for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[dt][qt][i] = 0.0f;
+  };
+  OTiles oacc;
+  zero_o(oacc);
+  float m_run[2] = {0.0f, 0.0f};
+  float l_run[2] = {0.0f, 0.0f};
   bool first = true;
   const float sl2 = p.scale_log2;
 
@@ -707,11 +772,12 @@ void attn_half_kernel(AttnParams p) {
   const int j0 = list.count_below(n0, p.gk);
   const bool one_chunk = p.top_k <= 64;
   const int r0 = j0 & 63;
-  uint64_t rem = 0;
+  uint64_t rem0 = 0;
   if (one_chunk) {
     const uint64_t v = list.valid;
-    rem = r0 == 0 ? v : (v >> r0) | (v << (64 - r0));
+    rem0 = r0 == 0 ? v : (v >> r0) | (v << (64 - r0));
   }
+  uint64_t rem = rem0;
   auto next_rot = [&](int j) -> int {
     if (one_chunk) {
       if (rem == 0) return p.top_k;
@@ -728,174 +794,189 @@ void attn_half_kernel(AttnParams p) {
     return r < j0 ? r : p.top_k;
   };
 
-  int j = next_rot(-1);
-  int32_t tok = j < p.top_k ? list.token(j) : 0;
-  // Elements 0 and 1 of the ring: K(lo), V(lo) of the first block.
-  if (j < p.top_k) {
-    dma(tok, 0, 0, 0);
-    dma(tok, 0, 1, 1);
-  }
 #pragma unroll
-  for (int ks = 0; ks < D / 16; ++ks) asm volatile("" ::"v"(qf[ks]));
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) asm volatile("" ::"v"(qf[qt][ks]));
 
-  vec8 pf[2];  // P^T of the current half: key steps s = 0, 1
-  f32x16 sacc;
-  // One listed block.  Its elements are 4 (position in the walk) + t, so
-  // with PH = position mod 3 element t sits in slot (PH + t) mod 3 and the
-  // slot it frees for element t + 2 is (PH + t + 2) mod 3: with the walk
-  // unrolled three blocks deep, every slot address is a constant.
-  auto run_block = [&](auto phase) {
-    constexpr int PH = decltype(phase)::value;
-    const int jn = next_rot(j);
-    const bool more = jn < p.top_k;
-    const int32_t tokn = more ? list.token(jn) : 0;
+  vec8 pf[2];  // P^T of the current half, per query tile
+  f32x4 sacc[2][2];
+  // S^T of a 32-key K half tile at Ks.
+  auto qk = [&](const uint8_t* Ks) {
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      // ===== K half: S^T (32 keys x 32 queries) = K Q^T, then P.
-      wait_vmcnt<4>();  // this element landed; the next one may be in flight
-      __syncthreads();  // both halves landed; the slot of the previous element is free
-      {
-        // Element + 2: K(hi) of this block after K(lo); K(lo) of the next block after K(hi).
-        const int t = 2 * half;
-        if (half == 0) dma(tok, 1, 0, (PH + t + 2) % 3);
-        else if (more) dma(tokn, 0, 0, (PH + t + 2) % 3);
-      }
-      const uint8_t* Ks = ring + ((PH + 2 * half) % 3) * kSlotBytes;
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sacc[i] = 0.0f;
-      {
-        constexpr int kSteps = D / 16;
-        constexpr int kPf = 3;
-        vec8 kf[kSteps];
-        auto read_k = [&](int ks) {
-          kf[ks] = __builtin_bit_cast(
-              vec8, *reinterpret_cast<const u32x4*>(Ks + kaddr + 16 * ((2 * ks + g) ^ ksw0)));
-        };
+      for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-        for (int ks = 0; ks < kPf; ++ks) read_k(ks);
-        __builtin_amdgcn_sched_group_barrier(0x100, kPf, 0);
+        for (int i = 0; i < 4; ++i) sacc[kt][qt][i] = 0.0f;
+    constexpr int kReads = 2 * (D / 32);  // read r: D step r / 2, key tile r % 2
+    constexpr int kPf = 3;
+    vec8 kf[kReads];
+    auto read_k = [&](int r) {
+      kf[r] = __builtin_bit_cast(vec8,
+                                 *reinterpret_cast<const u32x4*>(Ks + kaddr[r / 2] + 4096 * (r % 2)));
+    };
 #pragma unroll
-        for (int ks = 0; ks < kSteps; ++ks) {
-          if (ks + kPf < kSteps) read_k(ks + kPf);
-          sacc = Mfma<T>::mma(kf[ks], qf[ks], sacc);
-          if (ks + kPf < kSteps) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        }
-      }
-      auto rowmax = [&]() {
-        float mx = fmax3(sacc[0], sacc[1], sacc[2]);
+    for (int r = 0; r < kPf; ++r) read_k(r);
+    __builtin_amdgcn_sched_group_barrier(0x100, kPf, 0);
 #pragma unroll
-        for (int i = 3; i < 15; i += 2) mx = fmax3(mx, sacc[i], sacc[i + 1]);
-        mx = fmax3(mx, sacc[15], sacc[15]);
-        return max_halves(mx) * sl2;
-      };
-      auto exps = [&]() {
-        float ls[2];
+    for (int r = 0; r < kReads; ++r) {
+      if (r + kPf < kReads) read_k(r + kPf);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+      for (int qt = 0; qt < 2; ++qt)
+        sacc[r % 2][qt] = Mfma16<T>::mma(kf[r], qf[qt][r / 2], sacc[r % 2][qt]);
+      if (r + kPf < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+  };
+  // Row max of query tile qt over the half (all four lane groups), unscaled.
+  auto rowmax = [&](int qt) {
+    float mx = fmax3(sacc[0][qt][0], sacc[0][qt][1], sacc[0][qt][2]);
+    mx = fmax3(mx, sacc[0][qt][3], sacc[1][qt][0]);
+    mx = fmax3(mx, sacc[1][qt][1], sacc[1][qt][2]);
+    mx = fmax3(mx, sacc[1][qt][3], sacc[1][qt][3]);
+    return max_quarters(mx);
+  };
+  // P of query tile qt against the offset m_run[qt]; returns the sum of its
+  // 8 (rounded) values.
+  auto exps = [&](int qt) {
 #pragma unroll
-          for (int jj = 0; jj < 8; ++jj)
-            pf[s][jj] = from_f32<T>(fast_exp2(fmaf(sacc[8 * s + jj], sl2, -m_run)));
-          ls[s] = Mfma<T>::sum8(pf[s], 0.0f);
-        }
-        return ls[0] + ls[1];
-      };
-      if (first) m_run = rowmax();
-      float ls = exps();
-      if (__ballot(!(ls <= kMaxTileSum))) {  // wave-uniform, rare
-        const float m_new = fmax3(m_run, rowmax(), m_run);
-        const float corr = fast_exp2(m_run - m_new);
-        l_run *= corr;
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int md = 0; md < D / 32; ++md)
+      for (int i = 0; i < 4; ++i)
+        pf[qt][4 * kt + i] = from_f32<T>(fast_exp2(fmaf(sacc[kt][qt][i], sl2, -m_run[qt])));
+    return Mfma<T>::sum8(pf[qt], 0.0f);
+  };
+  // O^T += V^T P^T over a 32-key V half tile at Vs.
+  auto pv = [&](const uint8_t* Vs, OTiles& o) {
+    constexpr int kDt = D / 16;
+    constexpr int kPf = 2;
+    vec8 vf[kDt];
+    auto read_v = [&](int dt) {
+      const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(Vs + vaddr(dt)));
+      const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(Vs + vaddr(dt) + 4096));
+      vf[dt] = __builtin_bit_cast(vec8, (short __attribute__((ext_vector_type(8)))){
+                                            lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+    };
 #pragma unroll
-          for (int i = 0; i < 16; ++i) oacc[md][i] *= corr;
-        m_run = m_new;
-        ls = exps();
-      }
-      l_run += ls;
-      first = false;
+    for (int dt = 0; dt < kPf; ++dt) read_v(dt);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPf, 0);
+#pragma unroll
+    for (int dt = 0; dt < kDt; ++dt) {
+      if (dt + kPf < kDt) read_v(dt + kPf);
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) o[dt][qt] = Mfma16<T>::mma(vf[dt], pf[qt], o[dt][qt]);
+      if (dt + kPf < kDt) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+  };
 
-      // ===== V half: O^T += V^T P^T over its 32 keys.
-      // In flight: this V [, the element after it].  The last element of the
-      // last block has nothing behind it.
-      if (half == 1 && !more)
-        wait_vmcnt<0>();
-      else
+  // Overflow guard.  A wave whose half-tile P sum passes kMaxTileSum (its
+  // offset, set by the first half, is too low for a later key) marks itself
+  // dirty and walks on.  If either wave of the workgroup is dirty, both find
+  // each row's exact maximum over all listed keys and walk again with it as
+  // the offset (every P <= 1).  Rescaling O inside the walk instead would
+  // cost the walk its register allocation.
+  __shared__ int wave_dirty[2];
+  bool redo = false;
+  for (;;) {
+    zero_o(oacc);
+    l_run[0] = l_run[1] = 0.0f;
+    first = !redo;
+    bool dirty = false;
+    rem = rem0;
+    int j = next_rot(-1);
+    int32_t tok = j < p.top_k ? list.token(j) : 0;
+    if (j < p.top_k) {
+      dma(tok, 0, 0, 0);
+      dma(tok, 0, 1, 1);
+    }
+    auto run_block = [&](auto phase) {
+      constexpr int PH = decltype(phase)::value;
+      const int jn = next_rot(j);
+      const bool more = jn < p.top_k;
+      const int32_t tokn = more ? list.token(jn) : 0;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        // ===== K half: S^T = K Q^T, then P.
         wait_vmcnt<4>();
-      __syncthreads();
-      {
-        // Element + 2: V(hi) of this block after V(lo); V(lo) of the next after V(hi).
-        const int t = 2 * half + 1;
-        if (half == 0) dma(tok, 1, 1, (PH + t + 2) % 3);
-        else if (more) dma(tokn, 0, 1, (PH + t + 2) % 3);
-      }
-      const uint8_t* Vs = ring + ((PH + 2 * half + 1) % 3) * kSlotBytes;
-      {
-        vec8 vf[2][D / 32];
-        auto read_v = [&](int s, vec8* dst) {
-#pragma unroll
-          for (int md = 0; md < D / 32; ++md) {
-            v4s half_lo, half_hi;
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-              const int row = 16 * s + 8 * hh + vrow0;
-              const int col = 32 * md + vcol0;
-              const int addr = row * (2 * D) + 16 * ((col / 8) ^ C::vswz(row)) + 2 * (col % 8);
-              const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(Vs + addr));
-              if (hh == 0) half_lo = r; else half_hi = r;
-            }
-            dst[md] = __builtin_bit_cast(
-                vec8, (short __attribute__((ext_vector_type(8)))){half_lo[0], half_lo[1], half_lo[2],
-                                                                  half_lo[3], half_hi[0], half_hi[1],
-                                                                  half_hi[2], half_hi[3]});
-          }
-        };
-        read_v(0, vf[0]);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * (D / 32), 0);
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          if (s + 1 < 2) read_v(s + 1, vf[1]);
-#pragma unroll
-          for (int md = 0; md < D / 32; ++md) {
-            oacc[md] = Mfma<T>::mma(vf[s][md], pf[s], oacc[md]);
-            if (s + 1 < 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          }
+        __syncthreads();
+        {
+          const int t = 2 * half;
+          if (half == 0) dma(tok, 1, 0, (PH + t + 2) % 3);
+          else if (more) dma(tokn, 0, 0, (PH + t + 2) % 3);
         }
+        qk(ring + ((PH + 2 * half) % 3) * kSlotBytes);
+        if (first) {
+          m_run[0] = rowmax(0) * sl2;
+          m_run[1] = rowmax(1) * sl2;
+        }
+        const float l0 = exps(0), l1 = exps(1);
+        if (__ballot(!(l0 + l1 <= kMaxTileSum))) dirty = true;  // wave-uniform, rare
+        l_run[0] += l0;
+        l_run[1] += l1;
+        first = false;
+
+        // ===== V half: O^T += V^T P^T over its 32 keys.
+        if (half == 1 && !more)
+          wait_vmcnt<0>();
+        else
+          wait_vmcnt<4>();
+        __syncthreads();
+        {
+          const int t = 2 * half + 1;
+          if (half == 0) dma(tok, 1, 1, (PH + t + 2) % 3);
+          else if (more) dma(tokn, 0, 1, (PH + t + 2) % 3);
+        }
+        pv(ring + ((PH + 2 * half + 1) % 3) * kSlotBytes, oacc);
+      }
+      j = jn;
+      tok = tokn;
+    };
+    while (j < p.top_k) {
+      run_block(Phase<0>{});
+      if (j >= p.top_k) break;
+      run_block(Phase<1>{});
+      if (j >= p.top_k) break;
+      run_block(Phase<2>{});
+    }
+    if (lane == 0) wave_dirty[wave] = dirty ? 1 : 0;
+    __syncthreads();  // every ring read done (no DMA is outstanding here); flags visible
+    if (redo || !(wave_dirty[0] | wave_dirty[1])) break;  // workgroup-uniform
+    // Exact row maxima: K half tiles through slot 0, one at a time.
+    float mx0 = -__builtin_inff(), mx1 = -__builtin_inff();
+    for (int jj = list.next(0, p.gk); jj < p.top_k; jj = list.next(jj + 1, p.gk)) {
+      const int32_t tk = list.token(jj);
+      for (int half = 0; half < 2; ++half) {
+        dma(tk, half, 0, 0);
+        wait_vmcnt<0>();
+        __syncthreads();  // both waves' rows landed
+        qk(ring);
+        mx0 = fmax3(mx0, rowmax(0), mx0);
+        mx1 = fmax3(mx1, rowmax(1), mx1);
+        __syncthreads();  // slot 0 read by both waves before it is loaded again
       }
     }
-    j = jn;
-    tok = tokn;
-  };
-  while (j < p.top_k) {
-    run_block(Phase<0>{});
-    if (j >= p.top_k) break;
-    run_block(Phase<1>{});
-    if (j >= p.top_k) break;
-    run_block(Phase<2>{});
+    m_run[0] = mx0 * sl2;
+    m_run[1] = mx1 * sl2;
+    redo = true;
   }
 
-  // ---- Normalise, stage the 64 x D output tile in the ring (slots 0-1),
-  // write whole rows.
-  const float l_tot = sum_halves(l_run);
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  __syncthreads();  // every ring read done (no DMA is outstanding here)
-  {
-    const int row = 32 * wave + l32;
+  // ---- Normalise and stage the 64 x D output tile in the ring (wave w's
+  // rows in bytes [8 KB w, 8 KB (w + 1))), then write whole rows.
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const float l_tot = sum_quarters(l_run[qt]);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    const int row = 32 * wave + 16 * qt + gi;
     uint8_t* orow = ring + row * (2 * D);
 #pragma unroll
-    for (int md = 0; md < D / 32; ++md) {
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        u32x2 w;
-        w[0] = bits16(from_f32<T>(oacc[md][4 * i4 + 0] * inv)) |
-               (bits16(from_f32<T>(oacc[md][4 * i4 + 1] * inv)) << 16);
-        w[1] = bits16(from_f32<T>(oacc[md][4 * i4 + 2] * inv)) |
-               (bits16(from_f32<T>(oacc[md][4 * i4 + 3] * inv)) << 16);
-        const int chunk = 4 * md + i4;
-        *reinterpret_cast<u32x2*>(orow + 16 * (chunk ^ C::kswz(row)) + 8 * g) = w;
-      }
+    for (int dt = 0; dt < D / 16; ++dt) {
+      u32x2 w;
+      w[0] = bits16(from_f32<T>(oacc[dt][qt][0] * inv)) | (bits16(from_f32<T>(oacc[dt][qt][1] * inv)) << 16);
+      w[1] = bits16(from_f32<T>(oacc[dt][qt][2] * inv)) | (bits16(from_f32<T>(oacc[dt][qt][3] * inv)) << 16);
+      const int chunk = 2 * dt + G / 2;  // D 16 dt + 4 G .. + 3
+      *reinterpret_cast<u32x2*>(orow + 16 * (chunk ^ C::kswz(row)) + 8 * (G % 2)) = w;
     }
   }
   __syncthreads();
