@@ -10,46 +10,34 @@
 // longcat_video/models/block_sparse_attention_metal.py:75-164, 572-712, 829-962)
 // gives the same result.
 //
-// MFMA kernels (fp16 / bf16, sm_scale >= 0): attn_half_kernel for D = 128
-// and attn_mfma_kernel for D = 64.  attn_mfma_kernel:
+// MFMA kernel (fp16 / bf16, sm_scale >= 0, D = 64 or 128): attn_half_kernel.
 //   * one workgroup (2 waves) per (b, h, q-block); wave w owns query rows
-//     32w..32w+31 of the block; several waves per SIMD are resident, so one
-//     wave's softmax overlaps another's MFMAs;
-//   * the wave's Q tile stays in registers as the B operand of
-//     S^T = K Q^T (v_mfma_f32_32x32x16_{f16,bf16}, fp32 accumulate);
-//   * S^T's accumulator layout (lane = query column; runs of 4 consecutive
-//     keys) is the B-operand layout of O^T = V^T P^T, so P never leaves
-//     registers and every lane owns one query row: the online-softmax max/sum
-//     need one cross-lane exchange (lane ^ 32, v_permlane32_swap) and the O
-//     rescale is lane-local;
-//   * the exponent offset m of a row is the max of its first tile; later
-//     tiles compute P = exp2(s*scale*log2e - m) without a max pass, and only
-//     when a tile's P sum exceeds 2^15 (a wave-uniform branch) is m raised to
-//     the tile max, O and l rescaled and the tile redone, so P <= 2^15 stays
-//     a normal fp16/bf16 value; its rounded copy feeds both the PV product
-//     and the row sum (v_dot2), so numerator and denominator agree;
-//   * K and V tiles go from HBM straight into LDS with buffer_load ... lds
-//     (no register staging), row-major with 16-byte chunks XOR-swizzled by
-//     row so that every operand read is bank-conflict free: K rows are read
-//     with ds_read_b128, V^T operands with ds_read_b64_tr_b16 (lane L of a
-//     16-lane group receives element L%4 of the rows read by lanes
-//     L/4 + {0,4,8,12}, i.e. 4 consecutive keys of one V column);
-//   * K(j+1) is fetched while tile j's softmax and PV run, V(j+1) while
-//     tile j+1's QK^T runs (single-buffered K and V, explicit vmcnt waits);
-//     workgroups are ordered so each XCD sweeps the q-blocks of one head
-//     (shared K/V in its L2), and each workgroup starts its ascending list at
-//     a block index set by its launch slot, so the workgroups resident on an
-//     XCD walk a narrow window of K/V blocks together;
+//     32w..32w+31 of the block; three (D = 128) or four (D = 64) waves per
+//     SIMD are resident, so one wave's softmax overlaps another's MFMAs;
+//   * each listed 64-key block is processed as two 32-key halves on
+//     16 x 16 x 32 MFMAs (fp32 accumulate); the wave's Q tile stays in
+//     registers as the B operand of S^T = K Q^T, and S^T's accumulator layout
+//     is the B-operand layout of O^T = V^T P^T after a fixed relabelling of
+//     the keys, so P never leaves registers;
+//   * the exponent offset m of a row is the max of its first half; later
+//     halves compute P = exp2(s*scale*log2e - m) without a max pass; P is
+//     rounded once, and its rounded copy feeds both the PV product and the
+//     row sum (v_dot2), so numerator and denominator agree; a half whose P sum
+//     would pass 2^15 sends the workgroup through an exact second walk;
+//   * K and V half tiles go from HBM straight into a three-slot LDS ring with
+//     buffer_load ... lds (no register staging), row-major with 16-byte chunks
+//     XOR-swizzled by row so that every operand read is bank-conflict free:
+//     K rows are read with ds_read_b128, V^T operands with ds_read_b64_tr_b16
+//     (lane L of a 16-lane group receives element L%4 of the rows read by
+//     lanes L/4 + {0,4,8,12}, i.e. 4 consecutive keys of one V column);
+//   * every half tile is fetched two ring elements ahead (explicit vmcnt
+//     waits); workgroups are ordered so each XCD sweeps the q-blocks of one
+//     head (shared K/V in its L2), and each workgroup starts its ascending
+//     list at a block index set by its launch slot, so the workgroups resident
+//     on an XCD walk a narrow window of K/V blocks together;
 //   * the routing list is read 64 entries at a time; each lane turns its entry
-//     into the block's first token once, so a tile costs one v_readlane;
+//     into the block's first token once, so a block costs one v_readlane;
 //   * the output tile is staged through LDS and written as whole rows.
-//
-// attn_half_kernel keeps that work unit, swizzled DMA and walk but processes
-// each 64-key block as two 32-key halves on 16 x 16 x 32 MFMAs, whose K and
-// V half tiles stream through a three-slot LDS ring; its smaller state fits
-// three waves per SIMD at D = 128.  Its offset guard differs: a wave whose
-// tile sum passes 2^15 does not rescale O in place; the workgroup finds the
-// exact row maxima and walks its list again (see its own comment).
 //
 // Vector-ALU kernel (any dtype, D in {16, 32, 64, 128, 256}, any scale): 64
 // rows x 4 lanes per workgroup, fp32 throughout; used for fp32 inputs, head
@@ -59,10 +47,9 @@
 namespace lcv {
 namespace {
 
-// MFMA kernels: bound on a tile's partial sum of P values, so that every P
-// stays <= 2^15, a normal fp16 value.  Past it attn_mfma_kernel redoes the
-// tile against a raised offset and attn_half_kernel walks again with the
-// exact row maxima.
+// MFMA kernel: bound on a half tile's partial sum of P values, so that every
+// P stays <= 2^15, a normal fp16 value.  Past it the workgroup walks again
+// with the exact row maxima.
 constexpr float kMaxTileSum = 32768.0f;
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit dwords (gfx9 family)
 
@@ -195,8 +182,8 @@ template <>
 struct Mfma<f16> {
   typedef f16x8 vec8;
   typedef _Float16 vec2 __attribute__((ext_vector_type(2)));
-  __device__ static f32x16 mma(vec8 a, vec8 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  __device__ static f32x4 mma(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
   // Sum of the 8 elements of v added to acc.
   __device__ static float sum8(vec8 v, float acc) {
@@ -214,8 +201,8 @@ template <>
 struct Mfma<bf16> {
   typedef bf16x8 vec8;
   typedef __bf16 vec2 __attribute__((ext_vector_type(2)));
-  __device__ static f32x16 mma(vec8 a, vec8 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  __device__ static f32x4 mma(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
   __device__ static float sum8(vec8 v, float acc) {
     const vec2 one = {(bf16)1.0f, (bf16)1.0f};
@@ -228,415 +215,55 @@ struct Mfma<bf16> {
   }
 };
 
-// Tile geometry.  A K or V tile is 64 rows x D elements, row-major, 2*D
-// bytes per row, DC = D/8 16-byte chunks per row.  Chunk c of row r is stored
-// at chunk position c ^ swz(r):
+// Tile geometry.  K and V rows are row-major in LDS, 2*D bytes per row,
+// DC = D/8 16-byte chunks per row.  Chunk c of row r is stored at chunk
+// position c ^ swz(r):
 //   K: swz = (r / RP) % DC          -- 16 rows read one chunk column: conflict free
-//   V: swz = 4 * ((r / RP) % (DC/4)) -- 4 rows x 4 chunks per 32-lane tr-read: conflict free
+//   V: swz = 2 * ((r / RP) % (DC/2)) -- 8 rows x 32 bytes per 32-lane tr-read: conflict free
 // where RP = 256 / (2*D) rows share one 256-byte bank span.
 template <typename T, int D>
 struct MfmaCfg {
   static constexpr int kThreads = 128;
   static constexpr int DC = D / 8;
   static constexpr int RP = 256 / (2 * D);
-  static constexpr int kRowsPerDma = 64 / DC;              // rows per 1 KB wave load
-  static constexpr int kDmaPerWave = 64 / kRowsPerDma / 2; // loads per wave per tile
-  static constexpr int kTileBytes = 64 * 2 * D;
+  static constexpr int kRowsPerDma = 64 / DC;  // rows per 1 KB wave load
   static_assert(D == 64 || D == 128, "MFMA tiling covers D = 64, 128");
   __device__ static int kswz(int r) { return (r / RP) % DC; }
-  __device__ static int vswz(int r) { return 4 * ((r / RP) % (DC / 4)); }
+  __device__ static int vswz(int r) { return 2 * ((r / RP) % (DC / 2)); }
 };
-
-// Waves per SIMD the register allocation must allow.  D = 64 holds three
-// (132 registers; its 16 KB of LDS per workgroup would allow eight
-// workgroups per CU): asking for four makes the allocator spill to scratch.
-// (D = 128 runs in attn_half_kernel; this kernel at D = 128 needs the
-// 256-register budget of two waves.)
-template <int D>
-struct MfmaOccupancy {
-  static constexpr int kWaves = D == 128 ? 2 : 3;
-};
-
-template <typename T, int D>
-__global__ __launch_bounds__(128)
-__attribute__((amdgpu_waves_per_eu(MfmaOccupancy<D>::kWaves, MfmaOccupancy<D>::kWaves)))
-void attn_mfma_kernel(AttnParams p) {
-  typedef MfmaCfg<T, D> C;
-  typedef typename Mfma<T>::vec8 vec8;
-  __shared__ __attribute__((aligned(1024))) uint8_t Ks[C::kTileBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t Vs[C::kTileBytes];
-
-  const int wid = xcd_linear_work_id(blockIdx.x, gridDim.x);
-  const int bh = wid / p.nb;
-  const int qb = p.order ? uniform_i32(p.order[wid]) : wid - bh * p.nb;
-  if ((uint32_t)qb >= (uint32_t)p.nb) return;  // a launch-order entry outside [0, nb): nothing to do
-  const int b = bh / p.H;
-  const int h = bh - b * p.H;
-  const int tid = threadIdx.x;
-  const int wave = uniform_i32(tid / 64);
-  const int lane = tid % 64;
-  const int l32 = lane % 32;
-  const int g = lane / 32;
-
-  const T* qbase = reinterpret_cast<const T*>(p.q) + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
-  const T* kbase = reinterpret_cast<const T*>(p.k) + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
-  const T* vbase = reinterpret_cast<const T*>(p.v) + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
-  T* obase = reinterpret_cast<T*>(p.out) + (int64_t)b * p.o_sb + (int64_t)h * p.o_sh;
-  const __amdgpu_buffer_rsrc_t krs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, (int)p.k_head_bytes, kBufferFlags);
-  const __amdgpu_buffer_rsrc_t vrs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, (int)p.v_head_bytes, kBufferFlags);
-
-  // The routing list's load goes out first, the Q loads behind it: the list
-  // is needed first (it names the first tile), the Q fragments only at the
-  // first QK^T.
-  TileList list(p.idx + ((int64_t)bh * p.nb + qb) * p.top_k, p.top_k, p.nk);
-
-  // ---- Q tile: B operand of S^T = K Q^T; lane holds Q[row][16ks + 8g .. +8].
-  const int32_t qtok = block_base_token(p.g, qb) + voxel_row_offset(p.g, 32 * wave + l32);
-  vec8 qf[D / 16];
-  {
-    const T* qrow = qbase + (int64_t)qtok * p.q_ss + 8 * g;
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
-      qf[ks] = __builtin_bit_cast(vec8, *reinterpret_cast<const u32x4*>(qrow + 16 * ks));
-  }
-  list.finish(p.gk);
-
-  // ---- Direct-to-LDS loads: wave load t fills LDS bytes [1024 t, 1024 t + 1024)
-  // = rows t*RPD .. +RPD; lane i writes chunk position i % DC of row
-  // t*RPD + i / DC and so fetches chunk (i % DC) ^ swz(row) of that row.
-  uint32_t kvo[C::kDmaPerWave], vvo[C::kDmaPerWave];
-#pragma unroll
-  for (int u = 0; u < C::kDmaPerWave; ++u) {
-    const int t = wave * C::kDmaPerWave + u;
-    const int row = t * C::kRowsPerDma + lane / C::DC;
-    const int pos = lane % C::DC;
-    const uint32_t tokoff = (uint32_t)voxel_row_offset(p.gk, row);
-    // Minus the load's immediate offset (1 KB x its place in a group of 4).
-    kvo[u] = (tokoff * (uint32_t)p.k_ss + 8u * (pos ^ C::kswz(row))) * sizeof(T) - 1024u * (u % 4);
-    vvo[u] = (tokoff * (uint32_t)p.v_ss + 8u * (pos ^ C::vswz(row))) * sizeof(T) - 1024u * (u % 4);
-  }
-  static_assert(C::kDmaPerWave % 4 == 0, "DMA loads go in groups of four per M0 value");
-  const uint32_t k_row_bytes = (uint32_t)p.k_ss * sizeof(T);
-  const uint32_t v_row_bytes = (uint32_t)p.v_ss * sizeof(T);
-  // tok: first token of the block (uniform).
-  auto dma_k = [&](int32_t tok) {
-    const int off = (int)((uint32_t)tok * k_row_bytes);
-#pragma unroll
-    for (int u = 0; u < C::kDmaPerWave; u += 4) {
-      const uint32_t m0v = lds_addr(Ks + 1024 * (wave * C::kDmaPerWave + u));
-      dma16<0>(krs, kvo[u], off, m0v);
-      dma16<1024>(krs, kvo[u + 1], off, m0v);
-      dma16<2048>(krs, kvo[u + 2], off, m0v);
-      dma16<3072>(krs, kvo[u + 3], off, m0v);
-    }
-  };
-  auto dma_v = [&](int32_t tok) {
-    const int off = (int)((uint32_t)tok * v_row_bytes);
-#pragma unroll
-    for (int u = 0; u < C::kDmaPerWave; u += 4) {
-      const uint32_t m0v = lds_addr(Vs + 1024 * (wave * C::kDmaPerWave + u));
-      dma16<0>(vrs, vvo[u], off, m0v);
-      dma16<1024>(vrs, vvo[u + 1], off, m0v);
-      dma16<2048>(vrs, vvo[u + 2], off, m0v);
-      dma16<3072>(vrs, vvo[u + 3], off, m0v);
-    }
-  };
-
-  // ---- Per-lane LDS read addresses (bytes).
-  // K operand (GEMM1): row 32mt + l32, chunk 2ks + g.
-  int kaddr[2];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) kaddr[mt] = (32 * mt + l32) * (2 * D);
-  const int ksw0 = C::kswz(l32);  // same swizzle for rows l32 and 32 + l32
-  // V^T operand (GEMM2), step s, half hh, d-tile md: lane i of 16-lane group G
-  // supplies row 16s + 8hh + 4g + i/4, columns 32md + 16(G%2) + 4(i%4) .. +3.
-  const int G = lane / 16, gi = lane % 16;
-  const int vrow0 = 4 * g + gi / 4;                       // + 16s + 8hh
-  const int vcol0 = 16 * (G % 2) + 4 * (gi % 4);           // + 32md (elements)
-
-  f32x16 oacc[D / 32];
-#pragma unroll
-  for (int md = 0; md < D / 32; ++md)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) oacc[md][i] = 0.0f;
-  float m_run = 0.0f;  // exponent offset of this row (set by the first tile)
-  float l_run = 0.0f;  // this lane's partial row sum
-  bool first = true;   // wave-uniform
-  const float sl2 = p.scale_log2;   // >= 0 on this path
-
-  // Tile order: the list rotated to start at the first entry >= n0, where
-  // n0 follows this workgroup's launch slot across [0, nk).  Workgroups that
-  // are resident together start near the same block index and then advance
-  // through their ascending lists at about the same pace, so together they
-  // sweep a narrow window of K/V blocks that stays in L2.  The softmax is
-  // order independent; the order is a function of blockIdx only.
-  constexpr int kResident = 128;  // workgroups resident per XCD (32 CUs x 4)
-  const int slot = blockIdx.x / kNumXcd;
-  const int n0 = (int)(((int64_t)(slot % kResident) * p.nk) / kResident);
-  const int j0 = list.count_below(n0, p.gk);
-  // Lists of at most 64 entries sit in one chunk: walk them with a 64-bit
-  // mask of the valid entries not yet visited, rotated so that bit b is
-  // entry (b + j0) mod 64 (entries >= top_k are never valid).
-  const bool one_chunk = p.top_k <= 64;
-  const int r0 = j0 & 63;  // j0 may equal top_k = 64: a full turn
-  uint64_t rem = 0;
-  if (one_chunk) {
-    const uint64_t v = list.valid;
-    rem = r0 == 0 ? v : (v >> r0) | (v << (64 - r0));
-  }
-  // Next valid position in rotated order after position j (j < 0: start);
-  // returns top_k at the end.
-  auto next_rot = [&](int j) -> int {
-    if (one_chunk) {
-      if (rem == 0) return p.top_k;
-      const int b = (int)__builtin_ctzll(rem);
-      rem &= rem - 1;
-      return (b + r0) & 63;
-    }
-    if (j < 0 || j >= j0) {
-      const int r = list.next(j < 0 ? j0 : j + 1, p.gk);
-      if (r < p.top_k) return r;
-      j = -1;
-    }
-    const int r = list.next(j + 1, p.gk);
-    return r < j0 ? r : p.top_k;
-  };
-  int j = next_rot(-1);
-  if (j < p.top_k) {
-    const int32_t tok = list.token(j);
-    dma_k(tok);
-    dma_v(tok);
-  }
-  // Consume the Q fragments here, behind the first tile's DMAs, so the
-  // compiler's own vmcnt bookkeeping retires these loads before the tile
-  // loop; inside the loop the only outstanding vector loads are the tile
-  // DMAs, waited on explicitly.
-#pragma unroll
-  for (int ks = 0; ks < D / 16; ++ks) asm volatile("" ::"v"(qf[ks]));
-  while (j < p.top_k) {
-    const int jn = next_rot(j);
-    const int32_t njn = jn < p.top_k ? list.token(jn) : 0;
-    // In flight (oldest first): K(j), V(j).
-    wait_vmcnt<C::kDmaPerWave>();
-    __syncthreads();  // K(j) in LDS for both waves
-
-    // S^T (64 keys x 32 queries) = K Q^T.
-    f32x16 sacc[2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sacc[mt][i] = 0.0f;
-    // K operand reads run kPf k-steps ahead of the MFMAs that consume them
-    // (scheduling groups keep the compiler from sinking them back), so the
-    // MFMA chain does not wait on LDS latency.
-    constexpr int kSteps = D / 16;
-    constexpr int kPf = kSteps < 4 ? kSteps : 4;
-    vec8 kf[2][kSteps];
-    auto read_k = [&](int ks) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-        kf[mt][ks] = __builtin_bit_cast(
-            vec8, *reinterpret_cast<const u32x4*>(Ks + kaddr[mt] + 16 * ((2 * ks + g) ^ ksw0)));
-    };
-#pragma unroll
-    for (int ks = 0; ks < kPf; ++ks) read_k(ks);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kPf, 0);  // DS reads
-#pragma unroll
-    for (int ks = 0; ks < kSteps; ++ks) {
-      if (ks + kPf < kSteps) read_k(ks + kPf);
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) sacc[mt] = Mfma<T>::mma(kf[mt][ks], qf[ks], sacc[mt]);
-      if (ks + kPf < kSteps) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
-    }
-    __syncthreads();  // both waves done reading K(j)
-    if (jn < p.top_k) dma_k(njn);  // overlaps softmax + PV
-
-    // Online softmax for this lane's query row (keys split between g = 0,
-    // 1).  The offset m_run is the row max of the first tile; later tiles
-    // are exponentiated against it directly, and only if a tile's P would
-    // exceed 2^15 (its partial sum says so; NaN included) is the offset
-    // raised to the tile max, O and l rescaled and the tile redone.  P stays
-    // a normal fp16/bf16 value, so no per-tile max is computed.
-    auto rowmax = [&]() {
-      float mx = fmax3(sacc[0][0], sacc[1][0], sacc[0][1]);
-      mx = fmax3(mx, sacc[1][1], sacc[1][1]);
-#pragma unroll
-      for (int i = 2; i < 16; ++i) mx = fmax3(mx, sacc[0][i], sacc[1][i]);
-      return max_halves(mx) * sl2;
-    };
-    // P^T as the B operand: step s takes accumulator values 8s .. 8s+7, the
-    // key runs 16s + 4g + {0..3} and 16s + 8 + 4g + {0..3}.
-    vec8 pf[4];
-    // The row sum is kept as four partial sums (one per PV step), so its
-    // dot products form four short dependency chains instead of one long one.
-    auto exps = [&]() {
-      float ls[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int flat = 8 * s + jj;
-          pf[s][jj] = from_f32<T>(fast_exp2(fmaf(sacc[flat / 16][flat % 16], sl2, -m_run)));
-        }
-        ls[s] = Mfma<T>::sum8(pf[s], 0.0f);
-      }
-      return (ls[0] + ls[2]) + (ls[1] + ls[3]);
-    };
-    if (first) m_run = rowmax();  // wave-uniform; O and l are still 0
-    float ls = exps();
-    if (__ballot(!(ls <= kMaxTileSum))) {  // wave-uniform, rare
-      const float m_new = fmax3(m_run, rowmax(), m_run);
-      const float corr = fast_exp2(m_run - m_new);
-      l_run *= corr;
-#pragma unroll
-      for (int md = 0; md < D / 32; ++md)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[md][i] *= corr;
-      m_run = m_new;
-      ls = exps();
-    }
-    l_run += ls;
-    first = false;
-
-    // In flight: V(j) [, K(j+1)].
-    if (jn < p.top_k)
-      wait_vmcnt<C::kDmaPerWave>();
-    else
-      wait_vmcnt<0>();
-    __syncthreads();  // V(j) in LDS for both waves
-
-    // O^T (D x 32 queries) += V^T P^T; V^T fragments of step s + 1 are read
-    // while the MFMAs of step s run.
-    {
-      vec8 vf[4][D / 32];
-      auto read_v = [&](int s) {
-#pragma unroll
-        for (int md = 0; md < D / 32; ++md) {
-          v4s half_lo, half_hi;
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            const int row = 16 * s + 8 * hh + vrow0;
-            const int col = 32 * md + vcol0;
-            const int addr = row * (2 * D) + 16 * ((col / 8) ^ C::vswz(row)) + 2 * (col % 8);
-            const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(Vs + addr));
-            if (hh == 0) half_lo = r; else half_hi = r;
-          }
-          vf[s][md] = __builtin_bit_cast(
-              vec8, (short __attribute__((ext_vector_type(8)))){half_lo[0], half_lo[1], half_lo[2],
-                                                                half_lo[3], half_hi[0], half_hi[1],
-                                                                half_hi[2], half_hi[3]});
-        }
-      };
-      read_v(0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * (D / 32), 0);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        if (s + 1 < 4) read_v(s + 1);
-#pragma unroll
-        for (int md = 0; md < D / 32; ++md) {
-          oacc[md] = Mfma<T>::mma(vf[s][md], pf[s], oacc[md]);
-          if (s + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        }
-      }
-    }
-    __syncthreads();  // both waves done reading V(j)
-    if (jn < p.top_k) dma_v(njn);  // overlaps the next QK^T
-    j = jn;
-  }
-
-  // ---- Normalise, stage the 64 x D output tile in LDS (K tile layout), then
-  // write whole rows: lane owns O[row][32md + 8(i/4) + 4g + (i%4)].
-  const float l_tot = sum_halves(l_run);
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  {
-    const int row = 32 * wave + l32;
-    uint8_t* orow = Ks + row * (2 * D);
-#pragma unroll
-    for (int md = 0; md < D / 32; ++md) {
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        u32x2 w;
-        w[0] = bits16(from_f32<T>(oacc[md][4 * i4 + 0] * inv)) |
-               (bits16(from_f32<T>(oacc[md][4 * i4 + 1] * inv)) << 16);
-        w[1] = bits16(from_f32<T>(oacc[md][4 * i4 + 2] * inv)) |
-               (bits16(from_f32<T>(oacc[md][4 * i4 + 3] * inv)) << 16);
-        const int chunk = 4 * md + i4;
-        *reinterpret_cast<u32x2*>(orow + 16 * (chunk ^ C::kswz(row)) + 8 * g) = w;
-      }
-    }
-  }
-  __syncthreads();
-  {
-    const int32_t tok0 = block_base_token(p.g, qb);
-#pragma unroll
-    for (int u = 0; u < 64 * C::DC / C::kThreads; ++u) {
-      const int pidx = tid + C::kThreads * u;
-      const int row = pidx / C::DC;
-      const int c = pidx % C::DC;
-      const int32_t tok = tok0 + voxel_row_offset(p.g, row);
-      *reinterpret_cast<u32x4*>(obase + (int64_t)tok * p.o_ss + 8 * c) =
-          *reinterpret_cast<const u32x4*>(Ks + row * (2 * D) + 16 * (c ^ C::kswz(row)));
-    }
-  }
-}
-
 
 // ---------------------------------------------------------------------------
-// Half-block MFMA kernel (fp16 / bf16, D = 128), three waves per SIMD.  The
-// work unit of attn_mfma_kernel (one workgroup of 2 waves per (b, h,
-// q-block), wave w owns query rows 32w .. 32w + 31), but each listed 64-key
-// block is processed as two 32-key halves, one after the other, and both
-// products run on 16 x 16 x 32 MFMAs.  Per wave and half:
+// Half-block MFMA kernel (fp16 / bf16, D = 64 or 128).  One workgroup of 2
+// waves per (b, h, q-block), wave w owns query rows 32w .. 32w + 31; each
+// listed 64-key block is processed as two 32-key halves, one after the other,
+// and both products run on 16 x 16 x 32 MFMAs.  Per wave and half:
 //   S^T[kt][qt] (16 keys x 16 queries) += K[kt] (16 x 32 of D) Q^T[qt] over
-//     4 D steps: 16 MFMAs; lane l holds query 16 qt + l % 16 and keys
+//     D / 32 D steps; lane l holds query 16 qt + l % 16 and keys
 //     16 kt + 4 (l / 16) + i;
-//   O^T[dt][qt] (16 of D x 16 queries) += V^T[dt] (16 x 32 keys) P^T[qt]:
-//     16 MFMAs.  P^T stays in registers as the B operand: its contraction
+//   O^T[dt][qt] (16 of D x 16 queries) += V^T[dt] (16 x 32 keys) P^T[qt],
+//     dt < D / 16.  P^T stays in registers as the B operand: its contraction
 //     index 8 (l / 16) + j stands for key 16 (j / 4) + 4 (l / 16) + j % 4,
 //     and the V^T operand is read from LDS in the same key order.
 // The 16 x 16 form reads a fifth fewer operand registers per FLOP than
 // 32 x 32 x 16, and on this power-limited chip that is time.  Each query's
 // keys sit in four lane groups (l, l ^ 16, l ^ 32, l ^ 48): the row max and
 // the final row sum reduce over all four (v_permlane16_swap, then
-// v_permlane32_swap).  A wave's state (Q 32, O 64, S 16, P 8 registers) fits
-// 168 registers.
+// v_permlane32_swap).  A wave's state (Q, O, S 16 and P 8 registers) fits 168
+// registers at D = 128 (three waves per SIMD) and 112 at D = 64 (four).
 //
-// The K and V half tiles (8 KB each) flow through a ring of three 8 KB LDS
-// slots, 24 KB per workgroup: six workgroups per CU.  Ring order, per block:
-// K(lo), V(lo), K(hi), V(hi).  Element e of that sequence sits in slot
-// e mod 3.  At the barrier that starts element e, both waves have consumed
-// element e - 1 and waited for their halves of e, so the DMA of element
-// e + 2 goes into e - 1's slot: every half tile is fetched two elements
-// ahead, with one barrier per element.  K rows keep the whole-block
-// kernel's swizzle; V rows are swizzled so that the 32 lanes of a
-// transposing read (8 rows x 32 bytes) hit distinct banks: chunk c of row r
-// sits at c ^ (2 (r mod 8)).  The launch slots rotate the walk as in
-// attn_mfma_kernel, over the 192 workgroups resident per XCD.
+// The K and V half tiles (32 rows each) flow through a ring of three LDS
+// slots, 24 KB per workgroup at D = 128: six workgroups per CU (eight at
+// D = 64).  Ring order, per block: K(lo), V(lo), K(hi), V(hi).  Element e of
+// that sequence sits in slot e mod 3.  At the barrier that starts element e,
+// both waves have consumed element e - 1 and waited for their halves of e,
+// so the DMA of element e + 2 goes into e - 1's slot: every half tile is
+// fetched two elements ahead, with one barrier per element.  The launch
+// slots rotate the walk over the workgroups resident per XCD: each starts its
+// ascending list at the first entry at or above (slot mod R) * nk / R.
 // ---------------------------------------------------------------------------
 template <int N>
 struct Phase {
   static constexpr int value = N;
-};
-
-template <typename T>
-struct Mfma16;
-
-template <>
-struct Mfma16<f16> {
-  __device__ static f32x4 mma(f16x8 a, f16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-
-template <>
-struct Mfma16<bf16> {
-  __device__ static f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
 };
 
 // Lanes l and l ^ 16 exchange x through v_permlane16_swap; the two results
@@ -658,13 +285,23 @@ __device__ __forceinline__ float sum_quarters(float x) {
   return sum_halves(a + b);
 }
 
-template <typename T>
-__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 3)))
+// Waves per SIMD for attn_half_kernel: D = 128 holds 168 registers per wave,
+// D = 64 (half the Q and O state) 128.
+template <int D>
+struct HalfOccupancy {
+  static constexpr int kWaves = D == 128 ? 3 : 4;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(128)
+__attribute__((amdgpu_waves_per_eu(HalfOccupancy<D>::kWaves, HalfOccupancy<D>::kWaves)))
 void attn_half_kernel(AttnParams p) {
-  constexpr int D = 128;
+  static_assert(D == 64 || D == 128, "half-block tiling covers D = 64, 128");
   typedef MfmaCfg<T, D> C;
   typedef typename Mfma<T>::vec8 vec8;
-  constexpr int kSlotBytes = 32 * 2 * D;  // 8 KB: 32 rows of K or V
+  constexpr int kSlotBytes = 32 * 2 * D;  // 32 rows of K or V: 8 KB at D = 128
+  constexpr int kGroup = 16 * 2 * D;      // bytes of 16 rows: the second key tile / key group
+  constexpr int kLoads = kSlotBytes / 1024 / 2;  // 1 KB DMA loads per wave per half tile
   __shared__ __attribute__((aligned(1024))) uint8_t ring[3 * kSlotBytes];
 
   const int wid = xcd_linear_work_id(blockIdx.x, gridDim.x);
@@ -702,52 +339,47 @@ void attn_half_kernel(AttnParams p) {
   }
   list.finish(p.gk);
 
-  // ---- DMA: a half tile is 32 rows (8 KB, 8 wave loads of 4 rows); wave w
-  // loads rows 16w .. 16w + 15 of it (4 loads).  Row r + 32 of a block sits
-  // voxel_row_offset(32) tokens after row r (voxel sides are powers of two),
-  // so the high half uses the low half's lane offsets plus a scalar.
-  auto vswz16 = [](int r) { return 2 * (r % 8); };
-  uint32_t kvo[4], vvo[4];
+  // ---- DMA: a half tile is 32 rows (2 kLoads wave loads of 1 KB); wave w
+  // loads rows 16w .. 16w + 15 of it (kLoads loads).  Row r + 32 of a block
+  // sits voxel_row_offset(32) tokens after row r (voxel sides are powers of
+  // two), so the high half uses the low half's lane offsets plus a scalar.
+  uint32_t kvo[kLoads], vvo[kLoads];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int t = 4 * wave + u;
+  for (int u = 0; u < kLoads; ++u) {
+    const int t = kLoads * wave + u;
     const int row = t * C::kRowsPerDma + lane / C::DC;  // 0 .. 31
     const int pc = lane % C::DC;
     const uint32_t tokoff = (uint32_t)voxel_row_offset(p.gk, row);
     kvo[u] = (tokoff * (uint32_t)p.k_ss + 8u * (pc ^ C::kswz(row))) * sizeof(T) - 1024u * u;
-    vvo[u] = (tokoff * (uint32_t)p.v_ss + 8u * (pc ^ vswz16(row))) * sizeof(T) - 1024u * u;
+    vvo[u] = (tokoff * (uint32_t)p.v_ss + 8u * (pc ^ C::vswz(row))) * sizeof(T) - 1024u * u;
   }
   const uint32_t k_row_bytes = (uint32_t)p.k_ss * sizeof(T);
   const uint32_t v_row_bytes = (uint32_t)p.v_ss * sizeof(T);
   const uint32_t hi_tok = (uint32_t)voxel_row_offset(p.gk, 32);
   auto dma = [&](int32_t tok, int half, int isv, int slot) {
     const uint32_t t = (uint32_t)tok + (half ? hi_tok : 0u);
-    const uint32_t m0v = lds_addr(ring + slot * kSlotBytes + 1024 * (4 * wave));
-    if (isv) {
-      const int off = (int)(t * v_row_bytes);
-      dma16<0>(vrs, vvo[0], off, m0v);
-      dma16<1024>(vrs, vvo[1], off, m0v);
-      dma16<2048>(vrs, vvo[2], off, m0v);
-      dma16<3072>(vrs, vvo[3], off, m0v);
-    } else {
-      const int off = (int)(t * k_row_bytes);
-      dma16<0>(krs, kvo[0], off, m0v);
-      dma16<1024>(krs, kvo[1], off, m0v);
-      dma16<2048>(krs, kvo[2], off, m0v);
-      dma16<3072>(krs, kvo[3], off, m0v);
+    const uint32_t m0v = lds_addr(ring + slot * kSlotBytes + 1024 * (kLoads * wave));
+    const __amdgpu_buffer_rsrc_t rs = isv ? vrs : krs;
+    const uint32_t* vo = isv ? vvo : kvo;
+    const int off = (int)(t * (isv ? v_row_bytes : k_row_bytes));
+    dma16<0>(rs, vo[0], off, m0v);
+    dma16<1024>(rs, vo[1], off, m0v);
+    if constexpr (kLoads == 4) {
+      dma16<2048>(rs, vo[2], off, m0v);
+      dma16<3072>(rs, vo[3], off, m0v);
     }
   };
 
   // LDS operand addresses.  K[kt] for D step ks: row 16 kt + gi (kt adds
-  // 4 KB), chunk 4 ks + G.  V^T[dt]: rows 4 G .. 4 G + 3 (+ 16 for the
-  // second key group, 4 KB further), columns 16 dt + 4 (gi % 4) .. + 3.
+  // kGroup bytes), chunk 4 ks + G.  V^T[dt]: rows 4 G .. 4 G + 3 (+ 16 for
+  // the second key group, kGroup further), columns 16 dt + 4 (gi % 4) .. + 3.
   // The swizzles XOR bit fields that nothing else in the address uses, so
   // the address of step ks (dt) is that of step 0 with 64 ks (32 dt) XORed in.
   int kaddr[D / 32];
 #pragma unroll
   for (int ks = 0; ks < D / 32; ++ks) kaddr[ks] = gi * (2 * D) + 16 * ((4 * ks + G) ^ C::kswz(gi));
   const int vrow = 4 * G + gi / 4;
-  const int vaddr0 = vrow * (2 * D) + 16 * (((4 * (gi % 4)) / 8) ^ vswz16(vrow)) + 2 * ((4 * (gi % 4)) % 8);
+  const int vaddr0 = vrow * (2 * D) + 16 * (((4 * (gi % 4)) / 8) ^ C::vswz(vrow)) + 2 * ((4 * (gi % 4)) % 8);
   auto vaddr = [&](int dt) { return vaddr0 ^ (32 * dt); };
 
   typedef f32x4 OTiles[D / 16][2];  // O^T tile (dt, qt)
@@ -766,7 +398,8 @@ void attn_half_kernel(AttnParams p) {
   bool first = true;
   const float sl2 = p.scale_log2;
 
-  constexpr int kResident = 192;  // workgroups resident per XCD (32 CUs x 6)
+  // Workgroups resident per XCD: 32 CUs x 4 SIMDs x kWaves / 2 waves each.
+  constexpr int kResident = 64 * HalfOccupancy<D>::kWaves;
   const int slot0 = blockIdx.x / kNumXcd;
   const int n0 = (int)(((int64_t)(slot0 % kResident) * p.nk) / kResident);
   const int j0 = list.count_below(n0, p.gk);
@@ -814,7 +447,7 @@ void attn_half_kernel(AttnParams p) {
     vec8 kf[kReads];
     auto read_k = [&](int r) {
       kf[r] = __builtin_bit_cast(vec8,
-                                 *reinterpret_cast<const u32x4*>(Ks + kaddr[r / 2] + 4096 * (r % 2)));
+                                 *reinterpret_cast<const u32x4*>(Ks + kaddr[r / 2] + kGroup * (r % 2)));
     };
 #pragma unroll
     for (int r = 0; r < kPf; ++r) read_k(r);
@@ -824,7 +457,7 @@ void attn_half_kernel(AttnParams p) {
       if (r + kPf < kReads) read_k(r + kPf);
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt)
-        sacc[r % 2][qt] = Mfma16<T>::mma(kf[r], qf[qt][r / 2], sacc[r % 2][qt]);
+        sacc[r % 2][qt] = Mfma<T>::mma(kf[r], qf[qt][r / 2], sacc[r % 2][qt]);
       if (r + kPf < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     }
@@ -854,7 +487,7 @@ void attn_half_kernel(AttnParams p) {
     vec8 vf[kDt];
     auto read_v = [&](int dt) {
       const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(Vs + vaddr(dt)));
-      const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(Vs + vaddr(dt) + 4096));
+      const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(Vs + vaddr(dt) + kGroup));
       vf[dt] = __builtin_bit_cast(vec8, (short __attribute__((ext_vector_type(8)))){
                                             lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
     };
@@ -865,7 +498,7 @@ void attn_half_kernel(AttnParams p) {
     for (int dt = 0; dt < kDt; ++dt) {
       if (dt + kPf < kDt) read_v(dt + kPf);
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) o[dt][qt] = Mfma16<T>::mma(vf[dt], pf[qt], o[dt][qt]);
+      for (int qt = 0; qt < 2; ++qt) o[dt][qt] = Mfma<T>::mma(vf[dt], pf[qt], o[dt][qt]);
       if (dt + kPf < kDt) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     }
@@ -899,7 +532,7 @@ void attn_half_kernel(AttnParams p) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         // ===== K half: S^T = K Q^T, then P.
-        wait_vmcnt<4>();
+        wait_vmcnt<kLoads>();
         __syncthreads();
         {
           const int t = 2 * half;
@@ -921,7 +554,7 @@ void attn_half_kernel(AttnParams p) {
         if (half == 1 && !more)
           wait_vmcnt<0>();
         else
-          wait_vmcnt<4>();
+          wait_vmcnt<kLoads>();
         __syncthreads();
         {
           const int t = 2 * half + 1;
@@ -1082,10 +715,7 @@ __global__ __launch_bounds__(256) void attn_valu_kernel(AttnParams p) {
 template <typename T, int D>
 hipError_t launch_mfma(const AttnParams& p, hipStream_t stream) {
   const int grid = p.B * p.H * p.nb;
-  if constexpr (D == 128)
-    hipLaunchKernelGGL((attn_half_kernel<T>), dim3(grid), dim3(128), 0, stream, p);
-  else
-    hipLaunchKernelGGL((attn_mfma_kernel<T, D>), dim3(grid), dim3(128), 0, stream, p);
+  hipLaunchKernelGGL((attn_half_kernel<T, D>), dim3(grid), dim3(128), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -523,54 +523,69 @@ def test_attention_launch_order_out_of_range_entries_launch_nothing(device, dtyp
     assert_close_report(_np(out), expect, *TOL[dtype], f"attn order with skipped entries {dtype}")
 
 
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("q_scale", [1.0, 6.0, 12.0])
-def test_attn_wide_score_range_rescales(device, dtype, q_scale):
+def test_attn_wide_score_range_rescales(device, dtype, q_scale, D):
     """Scores that grow along each routing list (K block j scaled by 1 + j/4)
     and large q scales push later tiles far above the first tile's max, so
-    the overflow guard acts: the D = 64 kernel raises the exponent offset
-    (and rescales O, l) many times per row, the D = 128 kernel walks the list
-    again with the exact row maxima."""
+    the overflow guard acts: the workgroup walks the list again with the
+    exact row maxima."""
     from lcv_bsa import bsa_attention_hip
 
     shape, chunk = (1, 1, 2048), (1, 1, 64)
     nb = 32
-    q = _rand((1, 2, 2048, 128), torch.float32, device, seed=31) * q_scale
-    k = _rand((1, 2, 2048, 128), torch.float32, device, seed=32)
+    q = _rand((1, 2, 2048, D), torch.float32, device, seed=31) * q_scale
+    k = _rand((1, 2, 2048, D), torch.float32, device, seed=32)
     k = k * (1.0 + torch.arange(2048, device=device).div(64, rounding_mode="floor").float() / 4.0)[None, None, :, None]
-    v = _rand((1, 2, 2048, 128), torch.float32, device, seed=33)
+    v = _rand((1, 2, 2048, D), torch.float32, device, seed=33)
     q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
     idx = np.broadcast_to(np.arange(0, nb, 2, dtype=np.int32), (1, 2, nb, nb // 2)).copy()
     idx[0, 1] = idx[0, 1, :, ::-1]  # descending lists too
     out = bsa_attention_hip(q, k, v, torch.from_numpy(idx).to(device), chunk, shape)
     ref = O.sparse_attention_from_indices(_np(q), _np(k), _np(v), idx, shape, chunk)
-    assert_close_report(_np(out), ref, *TOL[dtype], f"wide range q*{q_scale} {dtype}")
+    assert_close_report(_np(out), ref, *_wide_tol(dtype, D, q_scale), f"wide range q*{q_scale} {dtype} D={D}")
 
 
+def _wide_tol(dtype, D, q_scale):
+    """Tolerance of the wide-score-range tests.  With bf16 and D = 64 the
+    softmax over these growing scores is peaked enough that rounding P to
+    bf16 alone moves outputs by more than the general 1e-2: an ideal kernel
+    (exact row max, P rounded once to bf16, fp32 sums), emulated on the CPU
+    for these inputs, lands at 1.3-1.4e-2 max-abs against the fp64 oracle
+    for every q scale.  Those cases get 2e-2 max-abs; the mean-abs bound and
+    every other case keep the general tolerance."""
+    max_abs, mean_abs = TOL[dtype]
+    if dtype == torch.bfloat16 and D == 64:
+        max_abs = 2e-2
+    return max_abs, mean_abs
+
+
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("wide_rows", [(0, 32), (32, 64), (16, 48)])
-def test_attn_wide_range_in_some_rows_only(device, dtype, wide_rows):
+def test_attn_wide_range_in_some_rows_only(device, dtype, wide_rows, D):
     """Only some query rows of each 64-row block see the growing scores (q
-    scaled by 12 there), so in a D = 128 workgroup one wave overflows its
-    first-tile offset while the other does not (or both, for rows 16-48).
+    scaled by 12 there), so in a workgroup one wave overflows its first-tile
+    offset while the other does not (or both, for rows 16-48).
     Every row must still match the oracle, including the rows of a wave that
     had no overflow itself but walks again with its workgroup."""
     from lcv_bsa import bsa_attention_hip
 
     shape, chunk = (1, 1, 2048), (1, 1, 64)
     nb = 32
-    q = _rand((1, 2, 2048, 128), torch.float32, device, seed=41)
+    q = _rand((1, 2, 2048, D), torch.float32, device, seed=41)
     rows = torch.arange(2048, device=device) % 64
     q = q * torch.where((rows >= wide_rows[0]) & (rows < wide_rows[1]), 12.0, 1.0)[None, None, :, None]
-    k = _rand((1, 2, 2048, 128), torch.float32, device, seed=42)
+    k = _rand((1, 2, 2048, D), torch.float32, device, seed=42)
     k = k * (1.0 + torch.arange(2048, device=device).div(64, rounding_mode="floor").float() / 4.0)[None, None, :, None]
-    v = _rand((1, 2, 2048, 128), torch.float32, device, seed=43)
+    v = _rand((1, 2, 2048, D), torch.float32, device, seed=43)
     q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
     idx = np.broadcast_to(np.arange(0, nb, 2, dtype=np.int32), (1, 2, nb, nb // 2)).copy()
     idx[0, 1] = idx[0, 1, :, ::-1]
     out = bsa_attention_hip(q, k, v, torch.from_numpy(idx).to(device), chunk, shape)
     ref = O.sparse_attention_from_indices(_np(q), _np(k), _np(v), idx, shape, chunk)
-    assert_close_report(_np(out), ref, *TOL[dtype], f"wide range in rows {wide_rows} {dtype}")
+    assert_close_report(_np(out), ref, *_wide_tol(dtype, D, 12.0), f"wide range in rows {wide_rows} {dtype} D={D}")
     out2 = bsa_attention_hip(q, k, v, torch.from_numpy(idx).to(device), chunk, shape)
     assert torch.equal(out, out2), "second run differs"
 
