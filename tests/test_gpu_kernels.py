@@ -562,6 +562,27 @@ def _wide_tol(dtype, D, q_scale):
 
 
 @pytest.mark.parametrize("D", [64, 128])
+def test_attn_wide_range_long_lists(device, D):
+    """The overflow guard with lists longer than one 64-entry chunk (top-k 96
+    of 128 blocks, entries unsorted, one padding entry per row): the exact
+    pass and the second walk both cross chunk boundaries."""
+    from lcv_bsa import bsa_attention_hip
+
+    S, nb, k = 8192, 128, 96
+    shape, chunk = (1, 1, S), (1, 1, 64)
+    q = _rand((1, 2, S, D), torch.float32, device, seed=51) * 8.0
+    kk = _rand((1, 2, S, D), torch.float32, device, seed=52)
+    kk = kk * (1.0 + torch.arange(S, device=device).div(64, rounding_mode="floor").float() / 16.0)[None, None, :, None]
+    v = _rand((1, 2, S, D), torch.float32, device, seed=53)
+    q, kk, v = q.half(), kk.half(), v.half()
+    idx = _distinct_indices(1, 2, nb, nb, k, seed=54, sort=False)
+    idx[:, :, :, 5] = -1  # padding: skipped
+    out = bsa_attention_hip(q, kk, v, torch.from_numpy(idx).to(device), chunk, shape)
+    ref = O.sparse_attention_from_indices(_np(q), _np(kk), _np(v), idx, shape, chunk)
+    assert_close_report(_np(out), ref, *TOL[torch.float16], f"wide range, long lists, D={D}")
+
+
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("wide_rows", [(0, 32), (32, 64), (16, 48)])
 def test_attn_wide_range_in_some_rows_only(device, dtype, wide_rows, D):
