@@ -571,8 +571,13 @@ __global__ __launch_bounds__(256) void scores_kernel(RouteArgs a) {
   const float* qb = a.qbar + (int64_t)bh * a.nq * D;
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.kbar + (int64_t)bh * a.nk * D), (short)0, a.nk * D * 4, 0x00020000);
+  // The score resource covers this tile's rows only (at most 128 x 4096
+  // scores, 2 MiB), so byte offsets stay far below the drop offset whatever
+  // the head's nq x nk.
+  const int tile_rows = a.nq - rt * 128 < 128 ? a.nq - rt * 128 : 128;
   const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.score_out + (int64_t)bh * a.nq * a.nk), (short)0, a.nq * a.nk * 4, 0x00020000);
+      (void*)(a.score_out + ((int64_t)bh * a.nq + rt * 128) * a.nk), (short)0, tile_rows * a.nk * 4,
+      0x00020000);
 
   bf16x8 pa[KST][3];
   const bool a_bad = load_row_pieces<KST>(qb, row0, a.nq, D, 32, pa);
@@ -650,7 +655,8 @@ __global__ __launch_bounds__(256) void scores_kernel(RouteArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int row = row0 + 8 * (i / 4) + 4 * g + i % 4;
-        const uint32_t off = (row < a.nq && col < a.nk) ? (uint32_t)(row * a.nk + col) * 4u : kDrop;
+        const int trow = row - rt * 128;  // row within the tile's resource
+        const uint32_t off = (row < a.nq && col < a.nk) ? (uint32_t)(trow * a.nk + col) * 4u : kDrop;
         // Through a scalar: a vector element subscript passed straight to
         // __builtin_bit_cast is read as element 0 by this compiler.
         const float v = acc[t][i];

@@ -74,3 +74,32 @@ def gathered_attention_fp32(q, k, v, idx, scale, step=128):
                 p = torch.softmax(torch.bmm(qh[n0:n0 + n].contiguous(), kt) * scale, dim=-1)
                 out[b, h, n0 * 64:(n0 + n) * 64] = torch.bmm(p, vg).reshape(n * 64, D)
     return out
+
+
+def wide_range_inputs(D: int, q_scale: float, dtype, seeds=(31, 32, 33), wide_rows=None):
+    """Inputs of the wide-score-range attention tests, built on the CPU:
+    q ~ N(0,1) scaled by q_scale (only on rows wide_rows[0] <= r % 64 <
+    wide_rows[1] when given), K block j scaled by 1 + j/4 (scores grow along
+    the list), v ~ N(0,1), rounded to ``dtype``; two heads over S = 2048
+    (32 blocks of 64), every q-block routed to the even blocks, ascending in
+    head 0 and descending in head 1.  Returns (q, k, v, idx [1,2,32,16])."""
+    import numpy as np
+    import torch
+
+    def rand(shape, seed):
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        return torch.randn(*shape, generator=g)
+
+    nb = 32
+    q = rand((1, 2, 2048, D), seeds[0])
+    if wide_rows is None:
+        q = q * q_scale
+    else:
+        rows = torch.arange(2048) % 64
+        q = q * torch.where((rows >= wide_rows[0]) & (rows < wide_rows[1]), q_scale, 1.0)[None, None, :, None]
+    k = rand((1, 2, 2048, D), seeds[1])
+    k = k * (1.0 + torch.arange(2048).div(64, rounding_mode="floor").float() / 4.0)[None, None, :, None]
+    v = rand((1, 2, 2048, D), seeds[2])
+    idx = np.broadcast_to(np.arange(0, nb, 2, dtype=np.int32), (1, 2, nb, nb // 2)).copy()
+    idx[0, 1] = idx[0, 1, :, ::-1]  # descending lists too
+    return q.to(dtype), k.to(dtype), v.to(dtype), idx
