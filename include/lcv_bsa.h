@@ -114,7 +114,10 @@ int lcv_bsa_select(const float* qbar, const float* kbar, int64_t B, int64_t H,
  * q-blocks sorted by (first, middle) entry of their routing lists, so that
  * q-blocks whose ascending lists start together run together and share K/V
  * tiles in L2.  order is a dense [B,H,nq] int32.  Any permutation gives the
- * same attention result; this one only changes speed.  nq <= 4096.
+ * same attention result up to fp32 rounding (each workgroup starts its
+ * ascending list at an entry set by its launch slot, which changes the
+ * summation order); for a given order the result is deterministic.
+ * nq <= 4096.
  * No counterpart in the reference (its kernels launch in block order).
  */
 int lcv_bsa_schedule(const int32_t* idx, int64_t B, int64_t H, int64_t nq,
@@ -261,11 +264,19 @@ int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype,
  * the array holds the block scores of as many (b, h) pairs as fit, and the
  * routing runs as score GEMM + top-k over those slices when at most 8 cover
  * every head (720p, H=32: 3 slices), else as the fused select kernel that
- * keeps the scores on chip; every route gives the same routing.  The call
- * allocates and frees nothing.  Calls on one GPU share its array: calls
- * that overlap in time on one GPU (other streams, other threads) race and
- * must be serialised by the caller.  Nothing in the array carries over from
- * one call to the next (each call writes every byte it reads).
+ * keeps the scores on chip.  At D = 64 or 128 with num_blocks <= 2048 the
+ * fused kernel computes every score with the same split-bf16 MFMA sequence
+ * as the score GEMM, so both routes select the same blocks; elsewhere the
+ * fused kernel sums in fp32 on the vector ALU, and two scores within fp32
+ * rounding of each other may then be ordered differently than
+ * lcv_bsa_forward orders them.  The call allocates and frees nothing.  The
+ * first call on each device resolves the array's device address and must
+ * not be under stream capture (it returns LCV_BSA_ERR_UNSUPPORTED there,
+ * before any device work); later calls may be captured.  Calls on one GPU
+ * share its array: calls that overlap in time on one GPU (other streams,
+ * other threads) race and must be serialised by the caller.  Nothing in the
+ * array carries over from one call to the next (each call writes every byte
+ * it reads).
  */
 int lcv_bsa_forward_noalloc(const void* q, const void* k, const void* v,
                             int dtype, int64_t B, int64_t H, int64_t S,

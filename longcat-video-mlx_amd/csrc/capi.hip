@@ -421,7 +421,12 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-int scratch_on_current_device(void** out) {
+// The address is resolved on the first call on each device.  That call must
+// not be under stream capture: resolving the symbol may load the library's
+// code object onto the device, which a capture cannot record.  It is refused
+// there (before any device work), and every later call, captured or not,
+// uses the kept address.
+int scratch_on_current_device(hipStream_t stream, void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess)
@@ -432,6 +437,15 @@ int scratch_on_current_device(void** out) {
                 kMaxDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess)
+      return fail(LCV_BSA_ERR_LAUNCH, "lcv_bsa_forward_noalloc: hipStreamIsCapturing: %s",
+                  hipGetErrorString(e));
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(LCV_BSA_ERR_UNSUPPORTED,
+                  "lcv_bsa_forward_noalloc: the first call on device %d is under stream capture; "
+                  "call it once outside capture on that device first", dev);
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
@@ -498,7 +512,7 @@ int lcv_bsa_forward_noalloc(const void* q, const void* k, const void* v, int dty
   const int64_t score_bh = (int64_t)((kNoAllocScratchBytes - need) / slice);
   const bool sliced = score_bh > 0 && (B * H + score_bh - 1) / score_bh <= kMaxScoreSlices;
   void* base = nullptr;
-  if ((st = scratch_on_current_device(&base))) return st;
+  if ((st = scratch_on_current_device((hipStream_t)stream, &base))) return st;
   char* ws = reinterpret_cast<char*>(base);
   return run_forward(q, k, v, dtype, B, H, S, D, qs, ks, vs, top_k, sm_scale, g, nb, bs,
                      reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws + pb),

@@ -206,8 +206,11 @@ def select_block_indices(q_blocks: torch.Tensor, k_blocks: torch.Tensor, top_k: 
     """``topk_block_indices(block_routing_scores(q_blocks, k_blocks))``
     (attention.py:105-108).  By default in two kernels through a transient
     fp32 score tensor (the faster route at 720p sizes); ``fused=True`` runs
-    the single kernel that keeps the scores on chip.  Both give the same
-    selection."""
+    the single kernel that keeps the scores on chip.  At D = 64 or 128 with
+    nk <= 2048 both compute every score with the same split-bf16 MFMA
+    sequence and give the same selection; elsewhere the fused kernel sums in
+    fp32 on the vector ALU, so scores within fp32 rounding of each other may
+    be ordered differently."""
     _require_device(q_blocks, k_blocks)
     qb = q_blocks.float().contiguous()
     kb = k_blocks.float().contiguous()

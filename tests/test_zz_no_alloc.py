@@ -84,3 +84,112 @@ def test_noalloc_fused_route_when_score_slices_do_not_fit(device):
 
     lib = _lib.load()
     _compare(device, lib, 1, 56, (16, 45, 80), 128, torch.float16, 57, seed=33)
+
+
+def test_noalloc_graph_capture_replays_eager(device):
+    """lcv_bsa_forward_noalloc captured into a HIP graph (after an eager call
+    on the device resolved the scratch address) replays to the eager bits --
+    with eager no-allocation calls on other inputs between the replays, which
+    rewrite the shared scratch, and after the captured input changes in
+    place."""
+    from lcv_bsa import _lib
+    from lcv_bsa.workloads import make_inputs
+
+    lib = _lib.load()
+    B, H, D, top_k, grid = 1, 4, 128, 4, (4, 16, 64)
+    S = grid[0] * grid[1] * grid[2]
+    shape, chunk, nb = (1, 1, S), (1, 1, 64), S // 64
+    q, k, v, _ = make_inputs(B, H, D, shape, chunk, torch.float16, device, seed=41, grid=grid, margin_ks=(top_k,))
+    q2, k2, v2, _ = make_inputs(B, H, D, shape, chunk, torch.float16, device, seed=42, grid=grid, margin_ks=(top_k,))
+
+    def run(qq, kk, vv):
+        o = torch.empty_like(qq)
+        i = torch.empty((B, H, nb, top_k), dtype=torch.int32, device=device)
+        _lib.check(_call(lib, "lcv_bsa_forward_noalloc", qq, kk, vv, top_k, shape, chunk, o, i), "noalloc")
+        return o, i
+
+    eager_out, eager_idx = run(q, k, v)
+    eager2_out, eager2_idx = run(q2, k, v)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        run(q, k, v)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+
+    out = torch.empty_like(q)
+    idx = torch.empty((B, H, nb, top_k), dtype=torch.int32, device=device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = _call(lib, "lcv_bsa_forward_noalloc", q, k, v, top_k, shape, chunk, out, idx)
+    assert st == 0, lib.lcv_bsa_last_error()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager_out), f"replay {rep}: output"
+        assert torch.equal(idx, eager_idx), f"replay {rep}: routing"
+        other_out, _ = run(q2, k2, v2)  # eager call in between: rewrites the scratch
+        torch.cuda.synchronize()
+    q.copy_(q2)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager2_out) and torch.equal(idx, eager2_idx), "replay after input change"
+    print("no-alloc graph: 4 replays equal the eager results", flush=True)
+
+
+_FIRST_CALL_UNDER_CAPTURE = r"""
+import math, sys, torch
+sys.path[:0] = [{repo!r}, {pkg!r}]
+from lcv_bsa import _lib
+from lcv_bsa.block_sparse_attention import _geom, _strides
+from lcv_bsa.workloads import make_inputs
+lib = _lib.load()
+dev = torch.device("cuda", 0)
+B, H, D, top_k, grid = 1, 2, 64, 3, (2, 16, 64)
+S = grid[0] * grid[1] * grid[2]
+shape, chunk, nb = (1, 1, S), (1, 1, 64), S // 64
+q, k, v, _ = make_inputs(B, H, D, shape, chunk, torch.bfloat16, dev, seed=5, grid=grid, margin_ks=(top_k,))
+out = torch.empty_like(q)
+idx = torch.empty((B, H, nb, top_k), dtype=torch.int32, device=dev)
+def call():
+    s = torch.cuda.current_stream(dev).cuda_stream
+    return lib.lcv_bsa_forward_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.BF16, B, H, S, D,
+        _strides(q), _strides(k), _strides(v), top_k, 1.0 / math.sqrt(D), _geom(shape, chunk),
+        idx.data_ptr(), out.data_ptr(), _strides(out), s)
+pad = torch.zeros(16, device=dev)
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    pad.add_(1.0)
+    st = call()
+assert st == _lib.ERR_UNSUPPORTED, st
+assert b"under stream capture" in lib.lcv_bsa_last_error(), lib.lcv_bsa_last_error()
+assert call() == 0  # eager: resolves the address
+torch.cuda.synchronize()
+ref_out, ref_idx = out.clone(), idx.clone()
+out.zero_(); idx.zero_()
+g2 = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g2):
+    st = call()
+assert st == 0, lib.lcv_bsa_last_error()
+g2.replay()
+torch.cuda.synchronize()
+assert torch.equal(out, ref_out) and torch.equal(idx, ref_idx)
+print("child ok")
+"""
+
+
+def test_noalloc_first_call_under_capture_is_refused(device):
+    """In a fresh process, a first call on the device made under stream
+    capture is refused with LCV_BSA_ERR_UNSUPPORTED before any device work;
+    after one eager call, a captured call works and replays to its result."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    repo = Path(__file__).resolve().parents[1]
+    code = _FIRST_CALL_UNDER_CAPTURE.format(repo=str(repo), pkg=str(repo / "longcat-video-mlx_amd"))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and "child ok" in r.stdout
