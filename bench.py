@@ -213,15 +213,28 @@ def bench_prepare(lib, w, dev, stream, steps: int, warmup: int, seed: int):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n
 
+    # The box's own device-to-device copy of the bytes prepare_qk streams
+    # (q and k read once, written once): the practical rate of a read+write
+    # HBM pass on this GPU, timed in the same run.
+    esz = q.element_size()
+    half = 2 * B * H * S * D * esz
+    src = torch.empty((half,), dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+
+    def copy():
+        dst.copy_(src)
+
     for _ in range(warmup):
         fused()
+        copy()
     ms = timed(fused, steps)
+    ms_copy = timed(copy, steps)
     unfused()
     ms_torch = timed(unfused, max(2, steps // 4))
-    esz = q.element_size()
     nbytes = 2 * B * H * nb * (2 * 64 * D * esz + D * 4)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    del qkv, q_out, k_out
+    copy_gbs = 2 * half / (ms_copy * 1e-3) / 1e9
+    del qkv, q_out, k_out, src, dst
     torch.cuda.empty_cache()
     return {
         "kernel": "prep_kernel",
@@ -233,6 +246,10 @@ def bench_prepare(lib, w, dev, stream, steps: int, warmup: int, seed: int):
         "peak": 8000.0,
         "unit": "GB/s",
         "frac": round(gbs / 8000.0, 4),
+        "copy": {"what": f"device-to-device copy of {half} B (torch copy_, hipMemcpyAsync), "
+                         f"{2 * half} B of reads + writes", "ms": round(ms_copy, 4),
+                 "achieved": round(copy_gbs, 1), "unit": "GB/s"},
+        "frac_of_copy": round(gbs / copy_gbs, 4),
         "unfused_torch_ms": round(ms_torch, 4),
     }
 
@@ -288,6 +305,23 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int,
     mods = {"self_attn": blk.attn, "qkv_gemm": blk.attn.qkv, "proj_gemm": blk.attn.proj,
             "cross_attn": blk.cross_attn, "pre_cross_norm": blk.pre_crs_attn_norm, "ffn": blk.ffn}
     handles = []
+    # The two library calls between the QKV and proj GEMMs, timed the same
+    # way: prepare_qk (RMSNorm + RoPE + block means) and bsa_attention
+    # (routing from the means, launch order, attention kernel).
+    import lcv_bsa.dit_block as dbm
+    wrapped = {"prepare_qk": dbm.prepare_qk, "bsa_attention": dbm.bsa_attention}
+
+    def timed_call(name, fn):
+        def run(*a, **kw):
+            e0_, e1_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0_.record(stream)
+            r = fn(*a, **kw)
+            e1_.record(stream)
+            marks.setdefault(name, []).append([e0_, e1_])
+            return r
+        return run
+    for name, fn in wrapped.items():
+        setattr(dbm, name, timed_call(name, fn))
     for name, m in mods.items():
         def pre(mod, inp, name=name):
             e = torch.cuda.Event(enable_timing=True)
@@ -307,8 +341,10 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int,
     torch.cuda.synchronize()
     for h in handles:
         h.remove()
+    for name, fn in wrapped.items():
+        setattr(dbm, name, fn)
     per = {k: sum(a.elapsed_time(b) for a, b in v) / steps for k, v in marks.items()}
-    for k in mods:                     # sub-modules the fused path does not call
+    for k in list(mods) + list(wrapped):  # parts the fused path does not call
         per.setdefault(k, 0.0)
     ms_instr = b0.elapsed_time(b1) / steps
     bsa_ms = per["self_attn"] - per["qkv_gemm"] - per["proj_gemm"]
@@ -327,6 +363,11 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int,
         "ms": round(ms, 3),
         "bsa_ms": round(bsa_ms, 3),
         "bsa_share": round(bsa_ms / ms_instr, 4),
+        "bsa_parts_ms": {
+            "prepare_qk": round(per["prepare_qk"], 3),
+            "bsa_attention (routing + launch order + attention)": round(per["bsa_attention"], 3),
+            "between (host work with the GPU idle)": round(bsa_ms - per["prepare_qk"] - per["bsa_attention"], 3),
+        },
         "breakdown_ms": {
             "self_attn_qkv_gemm": round(per["qkv_gemm"], 3),
             "self_attn_bsa (prepare_qk + routing + attention)": round(bsa_ms, 3),
@@ -468,6 +509,24 @@ def bench_voxel_policy(lib, dev, stream, steps: int, warmup: int, seed: int):
     return {"workload": "latents (16, 48, 80) = 61440 tokens, B1 H32 D128 fp16, top-k 60 of 960, same inputs", **res}
 
 
+def run_leg(leg: str, lib, w, dev, stream, args, top_k: int) -> int:
+    """One secondary leg alone (the headline forward is not run): its JSON
+    object on one line."""
+    import torch
+
+    if leg == "prepare":
+        res = bench_prepare(lib, w, dev, stream, args.steps, args.warmup, args.seed)
+    elif leg == "kv_split":
+        res = bench_kv_split(lib, dev, stream, args.steps, args.warmup, args.seed)
+    elif leg == "block_geometry":
+        res = bench_voxel_policy(lib, dev, stream, args.steps, args.warmup, args.seed)
+    else:
+        dt = torch.float16 if leg == "dit_block" else torch.bfloat16
+        res = bench_dit_block(dev, stream, max(3, args.steps // 2), 2, args.seed, top_k, dt)
+    print(json.dumps({"leg": leg, **res}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -481,6 +540,9 @@ def main() -> int:
     ap.add_argument("--no-prepare", action="store_true", help="skip the pre-BSA prepare_qk timing")
     ap.add_argument("--no-dit-block", action="store_true", help="skip the 720p DiT block timing")
     ap.add_argument("--no-kv-split", action="store_true", help="skip the S_q != S_k (continuation) timing")
+    ap.add_argument("--leg", default=None,
+                    choices=["prepare", "kv_split", "block_geometry", "dit_block", "dit_block_bf16"],
+                    help="run only this leg (for profiling it alone) and print its JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (a known-size kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -527,6 +589,8 @@ def main() -> int:
         f"(margin repairs {w.repairs}, {time.time() - t0:.1f}s)")
 
     code = {"f16": _lib.F16, "bf16": _lib.BF16, "f32": _lib.F32}[dtype]
+    if args.leg is not None:
+        return run_leg(args.leg, lib, w, dev, torch.cuda.current_stream(dev), args, top_k)
     out = torch.empty_like(w.q)
     idx = torch.empty((B, H, nb, top_k), dtype=torch.int32, device=dev)
     ws_bytes = lib.lcv_bsa_forward_workspace_bytes(B, H, nb, D)
@@ -655,7 +719,8 @@ def main() -> int:
         pre = bench_prepare(lib, w, dev, stream, args.steps, args.warmup, args.seed)
         result["pre_bsa"] = pre
         log(f"pre-BSA prepare_qk {pre['ms']:.3f} ms ({pre['achieved']:.0f} GB/s, "
-            f"{100 * pre['frac']:.1f}% of HBM); unfused torch chain {pre['unfused_torch_ms']:.3f} ms")
+            f"{100 * pre['frac']:.1f}% of HBM, {100 * pre['frac_of_copy']:.1f}% of the box's copy rate "
+            f"{pre['copy']['achieved']:.0f} GB/s); unfused torch chain {pre['unfused_torch_ms']:.3f} ms")
     if args.config == "c2" and not args.no_kv_split:
         kv = bench_kv_split(lib, dev, stream, args.steps, args.warmup, args.seed)
         result["kv_split"] = kv

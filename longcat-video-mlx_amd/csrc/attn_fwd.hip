@@ -257,9 +257,10 @@ struct MfmaCfg {
 // that sequence sits in slot e mod 3.  At the barrier that starts element e,
 // both waves have consumed element e - 1 and waited for their halves of e,
 // so the DMA of element e + 2 goes into e - 1's slot: every half tile is
-// fetched two elements ahead, with one barrier per element.  The launch
-// slots rotate the walk over the workgroups resident per XCD: each starts its
-// ascending list at the first entry at or above (slot mod R) * nk / R.
+// fetched two elements ahead, with one barrier per element.  Each workgroup
+// starts its ascending list at the first entry at or above a block index set
+// by its launch slot (the sweep start, below), so that the workgroups
+// resident on an XCD walk one window of K/V blocks together.
 // ---------------------------------------------------------------------------
 template <int N>
 struct Phase {
@@ -401,10 +402,27 @@ void attn_half_kernel(AttnParams p) {
   bool first = true;
   const float sl2 = p.scale_log2;
 
-  // Workgroups resident per XCD: 32 CUs x 4 SIMDs x kWaves / 2 waves each.
+  // Sweep start.  Workgroups resident per XCD: 32 CUs x 4 SIMDs x kWaves /
+  // 2 waves each.  A workgroup walks its whole list (all nk blocks of the
+  // circle) in one lifetime T, so the XCD's resident workgroups share L2
+  // tiles when each starts where the sweep front is at its start time: the
+  // front is at 0 at launch and back at 0 after every lifetime.  Launch
+  // slot (generation g, index i) starts at about g T + s_g T (i / R - 1/2):
+  // the first generation starts together (s_0 = 0), and each later one
+  // spreads its starts over a wider window as the finishing times drift
+  // apart, s_g = min(1, 0.7 sqrt(g)) (fitted to measured start times).
+  // The start is a function of the launch slot only, so the walk order --
+  // and the result's bits -- do not depend on timing.
   constexpr int kResident = 64 * HalfOccupancy<D>::kWaves;
   const int slot0 = blockIdx.x / kNumXcd;
-  const int n0 = (int)(((int64_t)(slot0 % kResident) * p.nk) / kResident);
+  int n0;
+  {
+    const int gen = slot0 / kResident, i = slot0 - gen * kResident;
+    const float spread = fminf(1.0f, 0.7f * sqrtf((float)gen));
+    const float front = spread * (((float)i + 0.5f) / (float)kResident - 0.5f);
+    n0 = (int)floorf(front * (float)p.nk) % p.nk;
+    if (n0 < 0) n0 += p.nk;
+  }
   const int j0 = list.count_below(n0, p.gk);
   const bool one_chunk = p.top_k <= 64;
   const int r0 = j0 & 63;
