@@ -311,6 +311,8 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int,
     import lcv_bsa.dit_block as dbm
     wrapped = {"prepare_qk": dbm.prepare_qk, "bsa_attention": dbm.bsa_attention}
 
+    seen: dict = {}
+
     def timed_call(name, fn):
         def run(*a, **kw):
             e0_, e1_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -318,6 +320,7 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int,
             r = fn(*a, **kw)
             e1_.record(stream)
             marks.setdefault(name, []).append([e0_, e1_])
+            seen[name] = (a, kw, r)
             return r
         return run
     for name, fn in wrapped.items():
@@ -346,6 +349,47 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int,
     per = {k: sum(a.elapsed_time(b) for a, b in v) / steps for k, v in marks.items()}
     for k in list(mods) + list(wrapped):  # parts the fused path does not call
         per.setdefault(k, 0.0)
+    # The attention kernel alone on the block's own inputs and routing: with
+    # V as the block passes it (a strided view of the QKV output, token
+    # stride 3 H D) and with V copied head-major.
+    alone = None
+    if "bsa_attention" in seen:
+        import math as _m
+
+        from lcv_bsa import _lib
+        from lcv_bsa.block_sparse_attention import _geom, _strides
+        from lcv_bsa.block_sparse_attention_hip import schedule_block_order
+        (q_, k_, v_, shape_), kw_, (_, idx_) = seen["bsa_attention"]
+        order_ = schedule_block_order(idx_)
+        v_c = v_.contiguous()
+        o_ = torch.empty_like(q_)
+        lib = _lib.load()
+        code = {torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}[q_.dtype]
+        geom = _geom(shape_, kw_["chunk_thw"])
+        Bq, Hq, Sq, Dq = q_.shape
+
+        def attn_alone(vv):
+            _lib.check(lib.lcv_bsa_attn_fwd(
+                q_.data_ptr(), k_.data_ptr(), vv.data_ptr(), code, Bq, Hq, Sq, Dq, _strides(q_), _strides(k_),
+                _strides(vv), idx_.data_ptr(), order_.data_ptr(), idx_.shape[3], kw_["sm_scale"], geom,
+                o_.data_ptr(), _strides(o_), stream.cuda_stream), "attn")
+
+        def timed_alone(vv, n):
+            for _ in range(2):
+                attn_alone(vv)
+            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a0.record(stream)
+            for _ in range(n):
+                attn_alone(vv)
+            a1.record(stream)
+            torch.cuda.synchronize()
+            return a0.elapsed_time(a1) / n
+        n_alone = max(3, steps)
+        alone = {"v_strided_ms": round(timed_alone(v_, n_alone), 3),
+                 "v_contiguous_ms": round(timed_alone(v_c, n_alone), 3),
+                 "v_strides": list(v_.stride())}
+        del q_, k_, v_, v_c, o_, idx_, order_
+    seen.clear()
     ms_instr = b0.elapsed_time(b1) / steps
     bsa_ms = per["self_attn"] - per["qkv_gemm"] - per["proj_gemm"]
     Hf = blk.ffn.hidden_dim
@@ -368,6 +412,7 @@ def bench_dit_block(dev, stream, steps: int, warmup: int, seed: int, top_k: int,
             "bsa_attention (routing + launch order + attention)": round(per["bsa_attention"], 3),
             "between (host work with the GPU idle)": round(bsa_ms - per["prepare_qk"] - per["bsa_attention"], 3),
         },
+        "attention_alone_on_block_inputs": alone,
         "breakdown_ms": {
             "self_attn_qkv_gemm": round(per["qkv_gemm"], 3),
             "self_attn_bsa (prepare_qk + routing + attention)": round(bsa_ms, 3),

@@ -1,7 +1,9 @@
 // Launch order of the q-blocks of each head for the attention kernel.
 //
-// Any order gives bit-identical results (each q-block is computed by one
-// workgroup from its own routing list).  The order matters for the L2: each
+// Any order gives the same results up to fp32 rounding: each q-block is
+// computed by one workgroup from its own routing list, and its launch slot
+// sets where its walk over that list starts (the summation order).  For a
+// given order the result is deterministic.  The order matters for the L2: each
 // workgroup walks its KV blocks in ascending order, so workgroups that run at
 // the same time on an XCD re-read each other's K/V tiles from L2 when their
 // lists start at nearby blocks.  Sorting the q-blocks of a head by

@@ -37,8 +37,11 @@ def schedule_block_order(block_indices: torch.Tensor, num_kv_blocks: Optional[in
     q-blocks are sorted by the first and middle entries of their routing
     lists, so that blocks whose ascending lists start together run together
     and re-use each other's K/V tiles from L2.  Any order gives the same
-    attention output.  ``num_kv_blocks`` is the K/V block count the entries
-    index (default: nq, the S_q == S_k case).  nq <= 4096.
+    attention output up to fp32 rounding (a q-block's launch slot sets where
+    its walk over its list starts, which changes the summation order); for a
+    given order the result is deterministic.  ``num_kv_blocks`` is the K/V
+    block count the entries index (default: nq, the S_q == S_k case).
+    nq <= 4096.
     """
     _require_device(block_indices)
     bi = block_indices.to(torch.int32).contiguous()
