@@ -248,35 +248,47 @@ int lcv_bsa_forward(const void* q, const void* k, const void* v, int dtype,
                     void* stream);
 
 /* Bytes of device scratch lcv_bsa_forward_noalloc holds per GPU. */
-#define LCV_BSA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+#define LCV_BSA_NOALLOC_SCRATCH_BYTES ((size_t)1 << 20)
 
 /*
  * lcv_bsa_forward without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid allocation).  No counterpart in the
- * reference.  Same arguments and result as lcv_bsa_forward.  The pooled
- * means and the launch order live in a fixed device array of
- * LCV_BSA_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds
- * until the process ends:
- *   2 * round256(B*H*nb*D*4) + round256(B*H*nb*4) <= 64 MiB
- * (B*H*nb <= 65,280 at D = 128: both 720p configurations fit); larger
- * problems get LCV_BSA_ERR_UNSUPPORTED before any device work.  The rest of
- * the array holds the block scores of as many (b, h) pairs as fit, and the
- * routing runs as score GEMM + top-k over those slices when at most 8 cover
- * every head (720p, H=32: 3 slices), else as the fused select kernel that
- * keeps the scores on chip.  At D = 64 or 128 with num_blocks <= 2048 the
- * fused kernel computes every score with the same split-bf16 MFMA sequence
- * as the score GEMM, so both routes select the same blocks; elsewhere the
+ * reference.  Same arguments and result as lcv_bsa_forward.  The call
+ * allocates and frees nothing:
+ *   - the launch order (one int32 per (b, h, q-block)) lives in a fixed
+ *     device array of LCV_BSA_NOALLOC_SCRATCH_BYTES that every GPU the
+ *     library runs on holds until the process ends:
+ *     round256(B*H*nb*4) <= 1 MiB, i.e. B*H*nb <= 262,144 (720p at H=32,
+ *     nb=900: 28,800); larger problems get LCV_BSA_ERR_UNSUPPORTED before
+ *     any device work;
+ *   - the pooled means of q and k and the block scores are staged in out
+ *     before the attention overwrites every element of it.  out must
+ *     therefore be dense (its B*H*S*D elements fill one range, in any
+ *     order of the b, h, s dimensions; else LCV_BSA_ERR_LAYOUT) and must
+ *     overlap none of q, k, v, idx (else LCV_BSA_ERR_INVALID_ARG).
+ * out holds 64*D elements per block, the means 2*D floats, so the means
+ * always fit; the rest holds the block scores of as many (b, h) pairs as
+ * fit (every head at 720p), and the routing runs as score GEMM + top-k over
+ * those slices when at most 8 slices cover every head, else as the fused
+ * select kernel that keeps the scores on chip (with a 2-byte out, when
+ * num_blocks is above about 30*B*H*D or 240*D).  At D = 64 or 128 with num_blocks <= 2048 the fused
+ * kernel computes every score with the same split-bf16 MFMA sequence as
+ * the score GEMM, so both routes select the same blocks; elsewhere the
  * fused kernel sums in fp32 on the vector ALU, and two scores within fp32
  * rounding of each other may then be ordered differently than
- * lcv_bsa_forward orders them.  The call allocates and frees nothing.  The
- * first call on each device resolves the array's device address and must
- * not be under stream capture (it returns LCV_BSA_ERR_UNSUPPORTED there,
- * before any device work); later calls may be captured.  Calls on one GPU
- * share its array: calls that overlap in time on one GPU (other streams,
- * other threads) race and must be serialised by the caller.  Nothing in the
- * array carries over from one call to the next (each call writes every byte
- * it reads).
+ * lcv_bsa_forward orders them.
+ * The first call on each device resolves the array's device address and
+ * creates an event; it must not be under stream capture (it returns
+ * LCV_BSA_ERR_UNSUPPORTED there, before any device work); later calls may
+ * be captured.  Calls on one GPU share its array.  Uncaptured calls are
+ * ordered by the library: one on another stream than the previous
+ * uncaptured call waits (hipStreamWaitEvent) for that call's work, and
+ * calls from several host threads queue on a lock.  Captured calls are not:
+ * a graph replay that overlaps in time with another call on the same GPU
+ * races on the launch order, and the caller must order the two.  Nothing in
+ * the array carries over from one call to the next (each call writes every
+ * byte it reads).
  */
 int lcv_bsa_forward_noalloc(const void* q, const void* k, const void* v,
                             int dtype, int64_t B, int64_t H, int64_t S,

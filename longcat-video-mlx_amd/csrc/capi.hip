@@ -402,14 +402,16 @@ int run_forward(const void* q, const void* k, const void* v, int dtype, int64_t 
 }
 
 // ---------------------------------------------------------------------------
-// Device scratch of lcv_bsa_forward_noalloc: the pooled means of q and k and
-// the launch order, in a file-scope array that every GPU the library runs on
-// holds (its own copy) until the process ends.  Host code never passes the
+// Device scratch of lcv_bsa_forward_noalloc: the launch order (one int32 per
+// (b, h, q-block)), in a file-scope array that every GPU the library runs on
+// holds (its own copy) until the process ends.  The pooled means and block
+// scores are staged in the caller's out buffer instead (the attention, the
+// last kernel, overwrites every byte of it).  Host code never passes the
 // array's name to a kernel (on the host it is a stand-in, not a device
 // address): the device address comes from hipGetSymbolAddress, once per
 // device, with that device current, and is kept per device.
 // ---------------------------------------------------------------------------
-constexpr size_t kNoAllocScratchBytes = size_t{64} << 20;  // LCV_BSA_NOALLOC_SCRATCH_BYTES
+constexpr size_t kNoAllocScratchBytes = size_t{1} << 20;  // LCV_BSA_NOALLOC_SCRATCH_BYTES
 static_assert(kNoAllocScratchBytes == LCV_BSA_NOALLOC_SCRATCH_BYTES, "header and library agree");
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
@@ -417,16 +419,25 @@ static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 // routing; beyond it the single fused select launch is the faster route.
 constexpr int64_t kMaxScoreSlices = 8;
 
+// Per device: the array's address and an event recorded after each
+// uncaptured call's last launch, so that the next call, if it comes on
+// another stream, waits for the launch order that call still reads.
+struct NoAllocDevice {
+  void* scratch = nullptr;
+  hipEvent_t done = nullptr;
+  hipStream_t done_stream = nullptr;
+  bool recorded = false;
+};
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_noalloc_mu;  // held for a whole call: calls from several host threads queue
+NoAllocDevice g_noalloc[kMaxDevices];
 
-// The address is resolved on the first call on each device.  That call must
-// not be under stream capture: resolving the symbol may load the library's
-// code object onto the device, which a capture cannot record.  It is refused
-// there (before any device work), and every later call, captured or not,
-// uses the kept address.
-int scratch_on_current_device(hipStream_t stream, void** out) {
+// Set-up on the first call on each device: resolve the array's address and
+// create the ordering event.  That call must not be under stream capture:
+// resolving the symbol may load the library's code object onto the device,
+// which a capture cannot record.  It is refused there (before any device
+// work).  Caller holds g_noalloc_mu.
+int noalloc_device(bool capturing, NoAllocDevice** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess)
@@ -435,14 +446,9 @@ int scratch_on_current_device(hipStream_t stream, void** out) {
   if (dev < 0 || dev >= kMaxDevices)
     return fail(LCV_BSA_ERR_UNSUPPORTED, "lcv_bsa_forward_noalloc: device %d beyond %d", dev,
                 kMaxDevices);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    e = hipStreamIsCapturing(stream, &cs);
-    if (e != hipSuccess)
-      return fail(LCV_BSA_ERR_LAUNCH, "lcv_bsa_forward_noalloc: hipStreamIsCapturing: %s",
-                  hipGetErrorString(e));
-    if (cs != hipStreamCaptureStatusNone)
+  NoAllocDevice& d = g_noalloc[dev];
+  if (!d.scratch) {
+    if (capturing)
       return fail(LCV_BSA_ERR_UNSUPPORTED,
                   "lcv_bsa_forward_noalloc: the first call on device %d is under stream capture; "
                   "call it once outside capture on that device first", dev);
@@ -451,10 +457,46 @@ int scratch_on_current_device(hipStream_t stream, void** out) {
     if (e != hipSuccess || !p)
       return fail(LCV_BSA_ERR_LAUNCH, "lcv_bsa_forward_noalloc: hipGetSymbolAddress(scratch) on "
                   "device %d: %s", dev, hipGetErrorString(e));
-    g_scratch_ptr[dev] = p;
+    if (!d.done && (e = hipEventCreateWithFlags(&d.done, hipEventDisableTiming)) != hipSuccess) {
+      d.done = nullptr;
+      return fail(LCV_BSA_ERR_LAUNCH, "lcv_bsa_forward_noalloc: hipEventCreate on device %d: %s",
+                  dev, hipGetErrorString(e));
+    }
+    d.scratch = p;
   }
-  *out = g_scratch_ptr[dev];
+  *out = &d;
   return LCV_BSA_OK;
+}
+
+// Bytes from a [B, H, S, D] view's first element to one past its last.
+size_t view_span_bytes(int64_t B, int64_t H, int64_t S, int64_t D, const lcv_bsa_strides& s,
+                       size_t esz) {
+  return (size_t)((B - 1) * s.b + (H - 1) * s.h + (S - 1) * s.s + D) * esz;
+}
+
+bool ranges_overlap(const void* a, size_t an, const void* b, size_t bn) {
+  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+  return x < y + bn && y < x + an;
+}
+
+// True when the B*H*S*D elements of a [B, H, S, D] view (unit stride along
+// D) fill one contiguous range: the strides of the dimensions longer than 1,
+// taken in increasing order, are D, D times the first extent, and so on.
+bool dense_view(int64_t B, int64_t H, int64_t S, int64_t D, const lcv_bsa_strides& s) {
+  int64_t n[3] = {B, H, S}, st[3] = {s.b, s.h, s.s};
+  for (int i = 0; i < 3; ++i)
+    for (int j = i + 1; j < 3; ++j)
+      if (st[j] < st[i]) {
+        std::swap(st[i], st[j]);
+        std::swap(n[i], n[j]);
+      }
+  int64_t expect = D;
+  for (int i = 0; i < 3; ++i) {
+    if (n[i] == 1) continue;
+    if (st[i] != expect) return false;
+    expect *= n[i];
+  }
+  return true;
 }
 
 }  // namespace
@@ -494,31 +536,77 @@ int lcv_bsa_forward_noalloc(const void* q, const void* k, const void* v, int dty
   int st = check_forward_args(q, k, v, dtype, B, H, S, D, qs, ks, vs, top_k, sm_scale, g, idx, out,
                               os, &nb, &bs);
   if (st) return st;
-  // Every size is checked before the device is touched.
-  const size_t pb = pooled_bytes(B, H, nb, D);
-  const size_t need = 2 * pb + align256((size_t)B * H * nb * sizeof(int32_t));
-  if (need > kNoAllocScratchBytes)
+  // Every size, layout and overlap is checked before the device is touched.
+  const size_t order_bytes = align256((size_t)B * H * nb * sizeof(int32_t));
+  if (order_bytes > kNoAllocScratchBytes)
     return fail(LCV_BSA_ERR_UNSUPPORTED,
-                "lcv_bsa_forward_noalloc: the pooled means and launch order of B=%lld H=%lld "
-                "num_blocks=%lld D=%lld need %zu bytes, beyond its fixed device scratch of %zu "
-                "bytes; call lcv_bsa_forward with a workspace instead",
-                (long long)B, (long long)H, (long long)nb, (long long)D, need,
-                kNoAllocScratchBytes);
-  // The scratch left after the means and the launch order holds the block
-  // scores of score_bh (b, h) slices; the two-kernel routing runs slice by
-  // slice when a few slices cover every head (at 720p, H=32: 11 heads a
-  // slice, 3 slices), else the fused select kernel routes without scores.
+                "lcv_bsa_forward_noalloc: the launch order of B=%lld H=%lld num_blocks=%lld needs "
+                "%zu bytes, beyond its fixed device scratch of %zu bytes; call lcv_bsa_forward "
+                "with a workspace instead",
+                (long long)B, (long long)H, (long long)nb, order_bytes, kNoAllocScratchBytes);
+  // The pooled means and block scores are staged in out, which the
+  // attention overwrites last: out must be one dense range that no input
+  // and not idx overlaps.
+  if (!dense_view(B, H, S, D, os))
+    return fail(LCV_BSA_ERR_LAYOUT,
+                "lcv_bsa_forward_noalloc stages the pooled means and block scores in out: out "
+                "must be dense (strides b=%lld h=%lld s=%lld leave gaps); call lcv_bsa_forward "
+                "with a workspace instead", (long long)os.b, (long long)os.h, (long long)os.s);
+  const size_t esz = (size_t)elem_bytes(dtype);
+  const size_t out_bytes = (size_t)(B * H * S * D) * esz;
+  if (ranges_overlap(out, out_bytes, q, view_span_bytes(B, H, S, D, qs, esz)) ||
+      ranges_overlap(out, out_bytes, k, view_span_bytes(B, H, S, D, ks, esz)) ||
+      ranges_overlap(out, out_bytes, v, view_span_bytes(B, H, S, D, vs, esz)) ||
+      ranges_overlap(out, out_bytes, idx, (size_t)(B * H * nb * top_k) * sizeof(int32_t)))
+    return fail(LCV_BSA_ERR_INVALID_ARG,
+                "lcv_bsa_forward_noalloc stages the pooled means and block scores in out: out "
+                "must not overlap q, k, v or idx");
+  const uintptr_t out_addr = (uintptr_t)out, stage_addr = (out_addr + 255) & ~(uintptr_t)255;
+  const size_t stage_bytes = out_bytes - (size_t)(stage_addr - out_addr);
+  const size_t pb = pooled_bytes(B, H, nb, D);
+  if (2 * pb > stage_bytes)  // out holds 64*D elements per block, the means 2*D floats
+    return fail(LCV_BSA_ERR_UNSUPPORTED, "lcv_bsa_forward_noalloc: out too small for the means");
+  // What is left after the means holds the block scores of score_bh (b, h)
+  // slices; the two-kernel routing runs slice by slice when a few slices
+  // cover every head (at 720p, H=32, all heads in one slice), else the fused
+  // select kernel routes without scores.
   const size_t slice = align256((size_t)nb * nb * sizeof(float));
-  const int64_t score_bh = (int64_t)((kNoAllocScratchBytes - need) / slice);
+  const int64_t score_bh = (int64_t)((stage_bytes - 2 * pb) / slice);
   const bool sliced = score_bh > 0 && (B * H + score_bh - 1) / score_bh <= kMaxScoreSlices;
-  void* base = nullptr;
-  if ((st = scratch_on_current_device((hipStream_t)stream, &base))) return st;
-  char* ws = reinterpret_cast<char*>(base);
-  return run_forward(q, k, v, dtype, B, H, S, D, qs, ks, vs, top_k, sm_scale, g, nb, bs,
-                     reinterpret_cast<float*>(ws), reinterpret_cast<float*>(ws + pb),
-                     sliced ? reinterpret_cast<float*>(ws + need) : nullptr, score_bh,
-                     reinterpret_cast<int32_t*>(ws + 2 * pb), idx, out, os, (hipStream_t)stream,
-                     "lcv_bsa_forward_noalloc");
+  const hipStream_t s = (hipStream_t)stream;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s, &cs);
+  if (e != hipSuccess)
+    return fail(LCV_BSA_ERR_LAUNCH, "lcv_bsa_forward_noalloc: hipStreamIsCapturing: %s",
+                hipGetErrorString(e));
+  const bool capturing = cs != hipStreamCaptureStatusNone;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  NoAllocDevice* d = nullptr;
+  if ((st = noalloc_device(capturing, &d))) return st;
+  // An uncaptured call on another stream than the previous uncaptured call
+  // waits for that call's work: both use this device's launch order.
+  if (!capturing && d->recorded && d->done_stream != s &&
+      (e = hipStreamWaitEvent(s, d->done, 0)) != hipSuccess)
+    return fail(LCV_BSA_ERR_LAUNCH, "lcv_bsa_forward_noalloc: hipStreamWaitEvent: %s",
+                hipGetErrorString(e));
+  char* stage = reinterpret_cast<char*>(stage_addr);
+  st = run_forward(q, k, v, dtype, B, H, S, D, qs, ks, vs, top_k, sm_scale, g, nb, bs,
+                   reinterpret_cast<float*>(stage), reinterpret_cast<float*>(stage + pb),
+                   sliced ? reinterpret_cast<float*>(stage + 2 * pb) : nullptr, score_bh,
+                   reinterpret_cast<int32_t*>(d->scratch), idx, out, os, s,
+                   "lcv_bsa_forward_noalloc");
+  if (!capturing) {
+    if ((e = hipEventRecord(d->done, s)) != hipSuccess) {
+      d->recorded = false;
+      if (!st)
+        st = fail(LCV_BSA_ERR_LAUNCH, "lcv_bsa_forward_noalloc: hipEventRecord: %s",
+                  hipGetErrorString(e));
+    } else {
+      d->recorded = true;
+      d->done_stream = s;
+    }
+  }
+  return st;
 }
 
 int lcv_bsa_block_rows(const void* x, const void* a, int dtype, int64_t B, int64_t N, int64_t C,

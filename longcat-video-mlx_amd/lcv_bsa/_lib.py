@@ -24,6 +24,8 @@ ERR_DTYPE = 3
 ERR_UNSUPPORTED = 4
 ERR_LAYOUT = 5
 ERR_LAUNCH = 6
+# LCV_BSA_NOALLOC_SCRATCH_BYTES: the device array lcv_bsa_forward_noalloc holds per GPU
+NOALLOC_SCRATCH_BYTES = 1 << 20
 
 
 class Strides(ctypes.Structure):

@@ -113,6 +113,45 @@ def test_c_abi_validation_returns_before_launch():
                                     fake, None), "pool")
 
 
+@pytest.mark.skipif(not NO_GPU, reason="validation-only calls use fake pointers; CPU container only")
+def test_noalloc_validation_returns_before_launch():
+    """lcv_bsa_forward_noalloc refuses, before touching the device: a launch
+    order beyond its 1 MiB array, an out with gaps between its elements, and
+    an out overlapping q, k, v or idx (it stages the means and scores in out).
+    A dense out in [B, S, H, D] order passes every check and reaches the
+    first runtime call, which fails here without a GPU."""
+    from lcv_bsa import _lib
+
+    lib = _lib.load()
+    S_, G = _lib.Strides, _lib.Geom
+    assert _lib.NOALLOC_SCRATCH_BYTES == 1 << 20
+    gib = 1 << 30  # fake, 16-byte aligned, never dereferenced
+    q, k, v, out, idx = 1 * gib, 2 * gib, 3 * gib, 4 * gib, 5 * gib
+    B, H, S, D, top_k = 1, 4, 4096, 128, 4
+    dense = S_(H * S * D, S * D, D)
+
+    def call(out=out, os=dense, q=q, idx=idx, B=B, H=H, S=S):
+        qs = S_(H * S * D, S * D, D)
+        return lib.lcv_bsa_forward_noalloc(q, k, v, _lib.F16, B, H, S, D, qs, qs, qs, top_k, 0.1,
+                                           G(1, 1, S, 1, 1, 64), idx, out, os, None)
+
+    # B*H*nb = 8 * 40 * 900 = 288,000 int32 > 1 MiB
+    st = call(B=8, H=40, S=57600)
+    assert st == _lib.ERR_UNSUPPORTED and b"fixed device scratch" in lib.lcv_bsa_last_error()
+    assert call(os=S_(H * S * 2 * D, S * 2 * D, 2 * D)) == _lib.ERR_LAYOUT  # row gaps
+    assert call(os=S_(2 * H * S * D, S * D, D), B=2) == _lib.ERR_LAYOUT  # batch gap
+    assert b"dense" in lib.lcv_bsa_last_error()
+    out_bytes = B * H * S * D * 2
+    assert call(out=q) == _lib.ERR_INVALID_ARG and b"overlap" in lib.lcv_bsa_last_error()
+    assert call(out=q + out_bytes - 16) == _lib.ERR_INVALID_ARG  # last row of q
+    assert call(out=idx - out_bytes + 16) == _lib.ERR_INVALID_ARG  # first entries of idx
+    # Dense in [B, H, S, D] or [B, S, H, D] order (h stride D, s stride H*D),
+    # also with q ending right where out starts: passes every check.
+    for os, qq in ((dense, q), (S_(S * H * D, D, H * D), q), (dense, out - out_bytes)):
+        assert call(os=os, q=qq) == _lib.ERR_LAUNCH
+        assert b"hipStreamIsCapturing" in lib.lcv_bsa_last_error()
+
+
 def test_prepare_qk_validation_and_table_length():
     """lcv_bsa_prepare_qk argument checks (no launch) and the table size."""
     from lcv_bsa import _lib, rope_table

@@ -1,12 +1,16 @@
-"""lcv_bsa_forward_noalloc (no workspace, fixed device scratch) against
+"""lcv_bsa_forward_noalloc (no workspace: the launch order in a fixed 1 MiB
+device array, the pooled means and block scores staged in out) against
 lcv_bsa_forward (caller workspace), through the C ABI.
 
 Two calls in a row, the second on a smaller problem than the first, so the
-second reads a scratch array that still holds the first call's means and
-launch order: routing must be identical and the output bit-identical (same
-attention kernel, same routing, same launch order).  A problem beyond the
-scratch is refused with LCV_BSA_ERR_UNSUPPORTED (its tensors are sized for
-it, so nothing would read out of bounds even if it were not refused).
+second reads an array that still holds the first call's launch order:
+routing must be identical and the output bit-identical (same attention
+kernel, same routing, same launch order).  Also: an out in [B, S, H, D]
+order, the sliced and the fused routing, two calls on two streams with no
+synchronisation between them (the library orders them), graph capture, and
+a problem beyond the array (refused with LCV_BSA_ERR_UNSUPPORTED; its
+tensors are sized for it, so nothing would read out of bounds even if it
+were not refused).
 """
 
 from __future__ import annotations
@@ -34,56 +38,154 @@ def _call(lib, fn, q, k, v, top_k, shape, chunk, out, idx, ws=None):
     return getattr(lib, fn)(*args)
 
 
-def _compare(device, lib, B, H, grid, D, dtype, top_k, seed):
-    from lcv_bsa import _lib
+def _score_slices(B, H, nb, D, esz=2):
+    """(heads per score slice, slices) of the no-allocation routing for a
+    256-byte aligned out of B*H*nb*64*D elements of esz bytes; 0 slices
+    means the fused select kernel routes."""
+    r256 = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    left = B * H * nb * 64 * D * esz - 2 * r256(B * H * nb * D * 4)
+    per = left // r256(nb * nb * 4)
+    slices = -(-B * H // per) if per else 0
+    return per, (slices if slices <= 8 else 0)
+
+
+def _inputs(device, B, H, S, D, dtype, top_k, seed, grid):
     from lcv_bsa.workloads import make_inputs
 
-    S = grid[0] * grid[1] * grid[2]
-    shape, chunk = (1, 1, S), (1, 1, 64)
+    return make_inputs(B, H, D, (1, 1, S), (1, 1, 64), dtype, device, seed=seed, grid=grid,
+                       margin_ks=(top_k,))[:3]
+
+
+def _reference(device, lib, q, k, v, top_k):
+    from lcv_bsa import _lib
+
+    B, H, S, D = q.shape
     nb = S // 64
-    q, k, v, _ = make_inputs(B, H, D, shape, chunk, dtype, device, seed=seed, grid=grid, margin_ks=(top_k,))
     ws = torch.empty((lib.lcv_bsa_forward_workspace_bytes(B, H, nb, D),), dtype=torch.uint8, device=device)
     out_ref, idx_ref = torch.empty_like(q), torch.empty((B, H, nb, top_k), dtype=torch.int32, device=device)
-    _lib.check(_call(lib, "lcv_bsa_forward", q, k, v, top_k, shape, chunk, out_ref, idx_ref, ws), "forward")
-    out = torch.full_like(q, float("nan"))
+    _lib.check(_call(lib, "lcv_bsa_forward", q, k, v, top_k, (1, 1, S), (1, 1, 64), out_ref, idx_ref, ws),
+               "forward")
+    return out_ref, idx_ref
+
+
+def _empty_out(q, layout):
+    """out filled with NaN, as a [B, H, S, D] view of [B, H, S, D] or
+    [B, S, H, D] storage."""
+    B, H, S, D = q.shape
+    if layout == "bhsd":
+        return torch.full_like(q, float("nan"))
+    return torch.full((B, S, H, D), float("nan"), dtype=q.dtype, device=q.device).permute(0, 2, 1, 3)
+
+
+def _compare(device, lib, B, H, grid, D, dtype, top_k, seed, layout="bhsd", S=None):
+    from lcv_bsa import _lib
+
+    S = S or grid[0] * grid[1] * grid[2]
+    nb = S // 64
+    q, k, v = _inputs(device, B, H, S, D, dtype, top_k, seed, grid)
+    out_ref, idx_ref = _reference(device, lib, q, k, v, top_k)
+    out = _empty_out(q, layout)
     idx = torch.full((B, H, nb, top_k), -7, dtype=torch.int32, device=device)
-    _lib.check(_call(lib, "lcv_bsa_forward_noalloc", q, k, v, top_k, shape, chunk, out, idx), "forward_noalloc")
+    _lib.check(_call(lib, "lcv_bsa_forward_noalloc", q, k, v, top_k, (1, 1, S), (1, 1, 64), out, idx),
+               "forward_noalloc")
     torch.cuda.synchronize()
     assert torch.equal(idx, idx_ref), "routing differs"
     assert torch.equal(out, out_ref), "output differs"
-    print(f"no-alloc B{B} H{H} S{S} D{D} {dtype} top-k {top_k}: routing and output identical", flush=True)
+    per, slices = _score_slices(B, H, nb, D)
+    route = f"{slices} score slice(s) of {per} heads" if slices else "fused select"
+    print(f"no-alloc B{B} H{H} S{S} D{D} {dtype} top-k {top_k} out {layout}, {route}: "
+          "routing and output identical", flush=True)
 
 
 def test_noalloc_matches_forward_twice_second_smaller(device):
     from lcv_bsa import _lib
 
     lib = _lib.load()
-    # 720p headline shape first (29.6 MB of scratch), then a smaller problem.
+    # 720p headline shape first (every head's scores staged in out at once),
+    # then a smaller problem.
+    assert _score_slices(1, 32, 900, 128) == (136, 1)
     _compare(device, lib, 1, 32, (16, 45, 80), 128, torch.float16, 57, seed=31)
     _compare(device, lib, 1, 4, (2, 16, 64), 64, torch.bfloat16, 5, seed=32)
+
+
+def test_noalloc_out_in_bshd_order(device):
+    """out as a [B, H, S, D] view of [B, S, H, D] storage (the layout the DiT
+    block's projection reads): dense, so the means and scores are staged in
+    it; the result equals lcv_bsa_forward's into the same layout."""
+    from lcv_bsa import _lib
+
+    lib = _lib.load()
+    _compare(device, lib, 2, 8, (4, 16, 64), 128, torch.float16, 9, seed=34, layout="bshd")
 
 
 def test_noalloc_refuses_beyond_scratch(device):
     from lcv_bsa import _lib
 
     lib = _lib.load()
-    # B*H*nb = 2 * 64 * 900 = 115,200 > 65,280: 118 MB of means and order.
-    B, H, S, D, top_k = 2, 64, 57600, 128, 57
+    # B*H*nb = 5 * 64 * 900 = 288,000 > 262,144: a launch order beyond 1 MiB.
+    B, H, S, D, top_k = 5, 64, 57600, 64, 57
     q = torch.zeros((B, H, S, D), dtype=torch.float16, device=device)
     out = torch.empty_like(q)
     idx = torch.empty((B, H, S // 64, top_k), dtype=torch.int32, device=device)
     st = _call(lib, "lcv_bsa_forward_noalloc", q, q, q, top_k, (1, 1, S), (1, 1, 64), out, idx)
     assert st == _lib.ERR_UNSUPPORTED
     assert b"fixed device scratch" in lib.lcv_bsa_last_error()
+    st = _call(lib, "lcv_bsa_forward_noalloc", q, q, q, top_k, (1, 1, S), (1, 1, 64), q, idx)
+    assert st == _lib.ERR_UNSUPPORTED  # the size check comes first
 
 
-def test_noalloc_fused_route_when_score_slices_do_not_fit(device):
-    """56 heads at 720p leave scratch for 4 heads of block scores: 14 slices,
-    more than the sliced route takes, so the fused select kernel routes."""
+def test_noalloc_two_score_slices(device):
+    """2048 blocks at D=64, 16 heads: out holds the scores of 15 heads, so the
+    routing runs as two score GEMM + top-k slices."""
     from lcv_bsa import _lib
 
     lib = _lib.load()
-    _compare(device, lib, 1, 56, (16, 45, 80), 128, torch.float16, 57, seed=33)
+    assert _score_slices(1, 16, 2048, 64) == (15, 2)
+    _compare(device, lib, 1, 16, None, 64, torch.float16, 8, seed=35, S=2048 * 64)
+
+
+def test_noalloc_fused_route_when_scores_do_not_fit(device):
+    """2048 blocks at D=64, one head: one head's 16 MiB of scores do not fit
+    beside the means in its 16 MiB out, so the fused select kernel routes
+    (at num_blocks <= 2048 with the same split-bf16 MFMA scores)."""
+    from lcv_bsa import _lib
+
+    lib = _lib.load()
+    assert _score_slices(1, 1, 2048, 64) == (0, 0)
+    _compare(device, lib, 1, 1, None, 64, torch.bfloat16, 8, seed=33, S=2048 * 64)
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(device):
+    """Two calls on two streams with no synchronisation between them: the
+    second call's stream waits for the first call's work (both use the
+    device's launch-order array), so each result equals lcv_bsa_forward's.
+    Both problems have the same size, so every launch-order entry is in
+    range for either call."""
+    from lcv_bsa import _lib
+
+    lib = _lib.load()
+    B, H, D, top_k, grid = 1, 32, 128, 57, (16, 45, 80)
+    S = grid[0] * grid[1] * grid[2]
+    nb = S // 64
+    a = _inputs(device, B, H, S, D, torch.float16, top_k, 36, grid)
+    b = _inputs(device, B, H, S, D, torch.float16, top_k, 37, grid)
+    ref_a, ref_b = _reference(device, lib, *a, top_k), _reference(device, lib, *b, top_k)
+    outs = [torch.full_like(a[0], float("nan")) for _ in range(2)]
+    idxs = [torch.full((B, H, nb, top_k), -7, dtype=torch.int32, device=device) for _ in range(2)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=device) for _ in range(2)]
+    for rep in range(3):
+        for s, (q, k, v), o, i in zip(streams, (a, b), outs, idxs):
+            with torch.cuda.stream(s):
+                _lib.check(_call(lib, "lcv_bsa_forward_noalloc", q, k, v, top_k, (1, 1, S), (1, 1, 64), o, i),
+                           "forward_noalloc")
+        torch.cuda.synchronize()
+        for (out_ref, idx_ref), o, i, name in zip((ref_a, ref_b), outs, idxs, "ab"):
+            assert torch.equal(i, idx_ref), f"rep {rep} call {name}: routing"
+            assert torch.equal(o, out_ref), f"rep {rep} call {name}: output"
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+    print("no-alloc on two streams: 3 x 2 calls equal the workspace results", flush=True)
 
 
 def test_noalloc_graph_capture_replays_eager(device):
