@@ -15,9 +15,10 @@
 // top-k needs (lane l holds columns l, l+64, l+128, ...), so the fused path
 // never writes scores to memory.
 //
-// Top-k is an exact radix select on order-preserving 32-bit keys: a 32-step
+// Top-k is an exact radix select on order-preserving 32-bit keys: a bit-by-bit
 // binary search finds the k-th largest key with ballot/popcount counts (over
-// the keys above a cheap exact lower bound, compacted, when k <= 128), then
+// the keys above a cheap exact lower bound, compacted, when k <= 128; only
+// the bits below those the bound and the row maximum share), then
 // one ordered pass emits the indices of keys above it plus the lowest-index
 // keys equal to it, in ascending index order.  Equal scores therefore resolve
 // to the lower block index; NaN ranks below -inf; -0.0 equals +0.0.
@@ -48,14 +49,31 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
   return x;
 }
 
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t y = (uint32_t)__shfl_xor((int)x, o);
+    x = y > x ? y : x;
+  }
+  return x;
+}
+
 // Largest t with #(key >= t) >= k, built bit by bit over R keys per lane
-// (padding keys are 0 and never reach a candidate >= 1).  Once a candidate
-// at or above `floor` has exactly k keys at or above it, those keys are the
-// top k and the remaining bits cannot change the selection.
+// (padding keys are 0 and never reach a candidate >= 1).  `floor` is at most
+// the k-th largest key (#(key >= floor) >= k) and `hi` at least every key, so
+// the k-th largest key lies in [floor, hi] and carries the bits that floor
+// and hi share above their highest differing bit: the search starts with
+// those bits set as in floor (the bit-by-bit search from bit 31 would set
+// exactly them) and decides only the bits below.  Once a candidate at or
+// above `floor` has exactly k keys at or above it, those keys are the top k
+// and the remaining bits cannot change the selection.
 template <int R>
-__device__ uint32_t kth_key(const uint32_t (&key)[R], int k, uint32_t floor) {
-  uint32_t thr = 0u;
-  for (int bit = 31; bit >= 0; --bit) {
+__device__ uint32_t kth_key(const uint32_t (&key)[R], int k, uint32_t floor, uint32_t hi) {
+  const uint32_t diff = floor ^ hi;
+  if (diff == 0u) return floor;  // every key from floor to hi equals floor
+  const int top = 31 - __builtin_clz(diff);
+  uint32_t thr = floor & ~(uint32_t)((2ull << top) - 1ull);
+  for (int bit = top; bit >= 0; --bit) {
     const uint32_t cand = thr | (1u << bit);
     int cnt = 0;
 #pragma unroll
@@ -125,12 +143,13 @@ __device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out, 
   }
   constexpr int CAP = compact_cap<NPER>();
   if ((k <= 64 && nk >= 64) || (k <= 128 && nk >= 128)) {  // wave-uniform
-    uint32_t m = 0u;  // this lane's largest key (k <= 64) or second-largest key
+    uint32_t m = 0u;   // this lane's largest key (k <= 64) or second-largest key
+    uint32_t m1 = 0u;  // this lane's largest key
     if (k <= 64) {
 #pragma unroll
       for (int e = 0; e < NPER; ++e) m = key[e] > m ? key[e] : m;
+      m1 = m;
     } else {
-      uint32_t m1 = 0u;
 #pragma unroll
       for (int e = 0; e < NPER; ++e) {
         const uint32_t lo = key[e] < m1 ? key[e] : m1;
@@ -139,6 +158,7 @@ __device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out, 
       }
     }
     const uint32_t L = wave_min_u32(m);
+    const uint32_t hi = wave_max_u32(m1);  // the row's largest key
     int total = 0;
 #pragma unroll
     for (int e = 0; e < NPER; ++e) {
@@ -155,7 +175,7 @@ __device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out, 
       uint32_t ck[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) ck[r] = lane + 64 * r < total ? buf[lane + 64 * r] : 0u;
-      const uint32_t thr = kth_key<4>(ck, k, L);
+      const uint32_t thr = kth_key<4>(ck, k, L, hi);
       emit_selected<4>(ck, total, thr, k, out, [&](int r) { return (int32_t)buf[CAP + lane + 64 * r]; });
       return;
     }
@@ -163,12 +183,12 @@ __device__ void wave_topk(const float (&sc)[NPER], int nk, int k, int32_t* out, 
       uint32_t ck[8];
 #pragma unroll
       for (int r = 0; r < 8; ++r) ck[r] = lane + 64 * r < total ? buf[lane + 64 * r] : 0u;
-      const uint32_t thr = kth_key<8>(ck, k, L);
+      const uint32_t thr = kth_key<8>(ck, k, L, hi);
       emit_selected<8>(ck, total, thr, k, out, [&](int r) { return (int32_t)buf[CAP + lane + 64 * r]; });
       return;
     }
   }
-  const uint32_t thr = kth_key<NPER>(key, k, 0u);
+  const uint32_t thr = kth_key<NPER>(key, k, 0u, 0xffffffffu);
   emit_selected<NPER>(key, nk, thr, k, out, [&](int r) { return (int32_t)(r * 64 + lane); });
 }
 
@@ -619,48 +639,52 @@ __global__ __launch_bounds__(256) void scores_kernel(RouteArgs a) {
     const bool chunk_bad = __syncthreads_or(!fin) != 0;
     const bool bad = a_bad || chunk_bad;
     if (ch + 1 < ch1) load_chunk(ch + 1);
-    f32x16 acc[2];
+    // A wave whose 32 rows all lie past nq (the last row tile of a head)
+    // stages chunks and meets the barriers, but computes and stores nothing.
+    if (row0 < a.nq) {
+      f32x16 acc[2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
-    bf16x8 pb[2][3];
-    auto read_b = [&](int s, int t, bf16x8 (&dst)[3]) {
-      const int off = (32 * t + c) * RS + 32 * s + 16 * g;
+        for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+      bf16x8 pb[2][3];
+      auto read_b = [&](int s, int t, bf16x8 (&dst)[3]) {
+        const int off = (32 * t + c) * RS + 32 * s + 16 * g;
 #pragma unroll
-      for (int q = 0; q < 3; ++q) dst[q] = *reinterpret_cast<const bf16x8*>(&kp[q][off]);
-    };
-    if (!bad) {
-      read_b(0, 0, pb[0]);
+        for (int q = 0; q < 3; ++q) dst[q] = *reinterpret_cast<const bf16x8*>(&kp[q][off]);
+      };
+      if (!bad) {
+        read_b(0, 0, pb[0]);
 #pragma unroll
-      for (int s = 0; s < KST; ++s) {
-        read_b(s, 1, pb[1]);
-        tile_step(pa[s], pb[0], acc[0]);
-        if (s + 1 < KST) read_b(s + 1, 0, pb[0]);
-        tile_step(pa[s], pb[1], acc[1]);
+        for (int s = 0; s < KST; ++s) {
+          read_b(s, 1, pb[1]);
+          tile_step(pa[s], pb[0], acc[0]);
+          if (s + 1 < KST) read_b(s + 1, 0, pb[0]);
+          tile_step(pa[s], pb[1], acc[1]);
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < KST; ++s) {
+          read_b(s, 0, pb[0]);
+          read_b(s, 1, pb[1]);
+          tile_step_nf(pa[s], pb[0], acc[0]);
+          tile_step_nf(pa[s], pb[1], acc[1]);
+        }
       }
-    } else {
+      // Scores: rows row0 + 8 (i / 4) + 4 g + i % 4, columns ch * 64 + 32 t + c.
 #pragma unroll
-      for (int s = 0; s < KST; ++s) {
-        read_b(s, 0, pb[0]);
-        read_b(s, 1, pb[1]);
-        tile_step_nf(pa[s], pb[0], acc[0]);
-        tile_step_nf(pa[s], pb[1], acc[1]);
-      }
-    }
-    // Scores: rows row0 + 8 (i / 4) + 4 g + i % 4, columns ch * 64 + 32 t + c.
+      for (int t = 0; t < 2; ++t) {
+        const int col = ch * KC + 32 * t + c;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int col = ch * KC + 32 * t + c;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = row0 + 8 * (i / 4) + 4 * g + i % 4;
-        const int trow = row - rt * 128;  // row within the tile's resource
-        const uint32_t off = (row < a.nq && col < a.nk) ? (uint32_t)(trow * a.nk + col) * 4u : kDrop;
-        // Through a scalar: a vector element subscript passed straight to
-        // __builtin_bit_cast is read as element 0 by this compiler.
-        const float v = acc[t][i];
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), srs, off, 0, 0);
+        for (int i = 0; i < 16; ++i) {
+          const int row = row0 + 8 * (i / 4) + 4 * g + i % 4;
+          const int trow = row - rt * 128;  // row within the tile's resource
+          const uint32_t off = (row < a.nq && col < a.nk) ? (uint32_t)(trow * a.nk + col) * 4u : kDrop;
+          // Through a scalar: a vector element subscript passed straight to
+          // __builtin_bit_cast is read as element 0 by this compiler.
+          const float v = acc[t][i];
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), srs, off, 0, 0);
+        }
       }
     }
   }
@@ -680,8 +704,9 @@ hipError_t launch_scores_mfma(RouteArgs a, int BH, hipStream_t stream) {
 template <int NPER, int MODE>
 hipError_t launch_route_n(RouteArgs a, int BH, hipStream_t stream) {
   // Score rows per wave: the top-k alone runs one row per wave (more rows in
-  // flight hide its serial search); with the score GEMM, up to 4 rows share
-  // each staged key chunk.
+  // flight hide its serial search; two rows per wave measured slower at
+  // 14,400 rows and only 2-8 % faster at 28,800-57,600); with the score
+  // GEMM, up to 4 rows share each staged key chunk.
   constexpr int RW = (MODE == kTopkOnly || NPER > 32) ? 1 : (NPER <= 16 ? 4 : 2);
   a.tiles_per_bh = (a.nq + 4 * RW - 1) / (4 * RW);
   hipLaunchKernelGGL((route_kernel<NPER, RW, MODE>), dim3(BH * a.tiles_per_bh), dim3(256), 0,
