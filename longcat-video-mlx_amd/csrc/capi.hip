@@ -468,14 +468,18 @@ int noalloc_device(bool capturing, NoAllocDevice** out) {
   return LCV_BSA_OK;
 }
 
-// Bytes from a [B, H, S, D] view's first element to one past its last.
-size_t view_span_bytes(int64_t B, int64_t H, int64_t S, int64_t D, const lcv_bsa_strides& s,
-                       size_t esz) {
-  return (size_t)((B - 1) * s.b + (H - 1) * s.h + (S - 1) * s.s + D) * esz;
+// Bytes from a [B, H, S, D] view's first element to one past its last
+// (non-negative strides; 128-bit arithmetic, so no stride overflows it).
+unsigned __int128 view_span_bytes(int64_t B, int64_t H, int64_t S, int64_t D,
+                                  const lcv_bsa_strides& s, size_t esz) {
+  typedef unsigned __int128 u128;
+  return ((u128)(B - 1) * (u128)s.b + (u128)(H - 1) * (u128)s.h + (u128)(S - 1) * (u128)s.s +
+          (u128)D) * (u128)esz;
 }
 
-bool ranges_overlap(const void* a, size_t an, const void* b, size_t bn) {
-  const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+bool ranges_overlap(const void* a, unsigned __int128 an, const void* b, unsigned __int128 bn) {
+  typedef unsigned __int128 u128;
+  const u128 x = (uintptr_t)a, y = (uintptr_t)b;
   return x < y + bn && y < x + an;
 }
 

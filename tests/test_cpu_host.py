@@ -130,8 +130,8 @@ def test_noalloc_validation_returns_before_launch():
     B, H, S, D, top_k = 1, 4, 4096, 128, 4
     dense = S_(H * S * D, S * D, D)
 
-    def call(out=out, os=dense, q=q, idx=idx, B=B, H=H, S=S):
-        qs = S_(H * S * D, S * D, D)
+    def call(out=out, os=dense, q=q, idx=idx, B=B, H=H, S=S, qs=None):
+        qs = qs or S_(H * S * D, S * D, D)
         return lib.lcv_bsa_forward_noalloc(q, k, v, _lib.F16, B, H, S, D, qs, qs, qs, top_k, 0.1,
                                            G(1, 1, S, 1, 1, 64), idx, out, os, None)
 
@@ -145,6 +145,9 @@ def test_noalloc_validation_returns_before_launch():
     assert call(out=q) == _lib.ERR_INVALID_ARG and b"overlap" in lib.lcv_bsa_last_error()
     assert call(out=q + out_bytes - 16) == _lib.ERR_INVALID_ARG  # last row of q
     assert call(out=idx - out_bytes + 16) == _lib.ERR_INVALID_ARG  # first entries of idx
+    # A batch stride of 2^62 elements: the inputs' spans pass every address
+    # (computed without overflow), so they overlap out.
+    assert call(B=2, os=S_(H * S * D, S * D, D), qs=S_(1 << 62, S * D, D)) == _lib.ERR_INVALID_ARG
     # Dense in [B, H, S, D] or [B, S, H, D] order (h stride D, s stride H*D),
     # also with q ending right where out starts: passes every check.
     for os, qq in ((dense, q), (S_(S * H * D, D, H * D), q), (dense, out - out_bytes)):
