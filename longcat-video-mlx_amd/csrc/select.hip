@@ -421,6 +421,24 @@ __device__ __forceinline__ void tile_step(const bf16x8 (&a)[3], const bf16x8 (&b
   acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
 }
 
+// tile_step on two key tiles sharing the A pieces, the two accumulator
+// chains interleaved (each chain keeps tile_step's product order).
+__device__ __forceinline__ void tile_step2(const bf16x8 (&a)[3], const bf16x8 (&b)[3], const bf16x8 (&c)[3],
+                                           f32x16& acc, f32x16& acd) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+  acd = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], c[0], acd, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
+  acd = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], c[1], acd, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
+  acd = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], c[0], acd, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
+  acd = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], c[2], acd, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
+  acd = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], c[1], acd, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
+  acd = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], c[0], acd, 0, 0, 0);
+}
+
 // Piece 0 with its inf / NaN halves (bf16 exponent all ones) set to zero.
 __device__ __forceinline__ bf16x8 finite_part(const bf16x8& v) {
   u32x4 w = __builtin_bit_cast(u32x4, v);
@@ -654,13 +672,11 @@ __global__ __launch_bounds__(256) void scores_kernel(RouteArgs a) {
         for (int q = 0; q < 3; ++q) dst[q] = *reinterpret_cast<const bf16x8*>(&kp[q][off]);
       };
       if (!bad) {
-        read_b(0, 0, pb[0]);
 #pragma unroll
         for (int s = 0; s < KST; ++s) {
+          read_b(s, 0, pb[0]);
           read_b(s, 1, pb[1]);
-          tile_step(pa[s], pb[0], acc[0]);
-          if (s + 1 < KST) read_b(s + 1, 0, pb[0]);
-          tile_step(pa[s], pb[1], acc[1]);
+          tile_step2(pa[s], pb[0], pb[1], acc[0], acc[1]);
         }
       } else {
 #pragma unroll
