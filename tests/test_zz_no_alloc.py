@@ -118,6 +118,31 @@ def test_noalloc_out_in_bshd_order(device):
     _compare(device, lib, 2, 8, (4, 16, 64), 128, torch.float16, 9, seed=34, layout="bshd")
 
 
+def test_noalloc_out_off_a_256_byte_boundary(device):
+    """out 16 bytes past a 256-byte boundary (a view into a larger buffer):
+    the means and scores are staged from the next 256-byte boundary inside
+    out, and the bytes of the buffer outside out are left untouched."""
+    from lcv_bsa import _lib
+
+    lib = _lib.load()
+    B, H, D, top_k, grid = 1, 8, 128, 9, (4, 16, 64)
+    S = grid[0] * grid[1] * grid[2]
+    nb = S // 64
+    q, k, v = _inputs(device, B, H, S, D, torch.float16, top_k, 38, grid)
+    out_ref, idx_ref = _reference(device, lib, q, k, v, top_k)
+    n = B * H * S * D
+    buf = torch.full((n + 256,), 7.0, dtype=torch.float16, device=device)
+    assert buf.data_ptr() % 256 == 0
+    out = buf[8:8 + n].view(B, H, S, D)  # 16 bytes past the boundary
+    idx = torch.full((B, H, nb, top_k), -7, dtype=torch.int32, device=device)
+    _lib.check(_call(lib, "lcv_bsa_forward_noalloc", q, k, v, top_k, (1, 1, S), (1, 1, 64), out, idx),
+               "forward_noalloc")
+    torch.cuda.synchronize()
+    assert torch.equal(idx, idx_ref), "routing differs"
+    assert torch.equal(out, out_ref), "output differs"
+    assert bool((buf[:8] == 7.0).all()) and bool((buf[8 + n:] == 7.0).all()), "bytes outside out changed"
+
+
 def test_noalloc_refuses_beyond_scratch(device):
     from lcv_bsa import _lib
 
