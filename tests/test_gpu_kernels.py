@@ -245,6 +245,32 @@ def test_topk_lower_bound_paths(device, nk):
         assert np.array_equal(got.cpu().numpy(), ref), f"nk={nk} k={k}"
 
 
+@pytest.mark.parametrize("nk", [64, 900, 2048])
+def test_topk_shared_prefix_rows(device, nk):
+    """Rows whose candidate keys share long leading bit runs, where the
+    search starts far below bit 31: one exponent (30 + small steps), values
+    a few ulps apart, all-negative rows, and rows equal but for a few
+    columns."""
+    from lcv_bsa import topk_block_indices
+
+    rng = np.random.default_rng(300 + nk)
+    rows = []
+    rows.append(30.0 + rng.random(nk))                                     # one exponent
+    rows.append(np.float32(30.0) + rng.integers(0, 64, nk) * np.float32(2.0 ** -18))  # few-ulp steps
+    rows.append(-1.0 - rng.random(nk))                                     # all negative, one exponent
+    rows.append(-(2.0 ** -20) * (1 + rng.integers(0, 8, nk)))              # tiny negatives
+    r = np.full(nk, 3.25)
+    r[rng.integers(0, nk, 5)] = 3.5                                        # equal but for a few
+    rows.append(r)
+    rows.append(np.float32(1.0) + np.arange(nk) * np.float32(2.0 ** -23))  # consecutive floats
+    sc = np.stack(rows).astype(np.float32)[None, None]
+    sct = torch.from_numpy(sc).to(device)
+    for k in sorted({1, 5, 6, 29, 57, 63, 64, 65, 113, 128} & set(range(1, nk + 1))):
+        got, _ = topk_block_indices(sct, 0.0, top_k=k)
+        ref, _ = O.topk_block_indices(sc, top_k=k)
+        assert np.array_equal(got.cpu().numpy(), ref), f"nk={nk} k={k}"
+
+
 def test_topk_count_rule(device):
     """test_bsa_tier_a_smoke.py:78-94 on the HIP top-k."""
     from lcv_bsa import topk_block_indices
